@@ -1,0 +1,173 @@
+/*
+ * kvszp.h -- C ABI of the MI355X batched fixed-mode BF16 KV-page codec.
+ *
+ * Drop-in boundary for the reference's pybind11 module `cuszp_wrapper_cpp`
+ * (integration/cuszp_wrapper/pybind11_bindings.cpp) and the C++ class behind
+ * it (integration/cuszp_wrapper/cuszp_wrapper.h:9-158).  Every entry point
+ * takes plain pointers and sizes; no framework types cross this boundary.
+ *
+ * Conventions shared by all entry points:
+ *  - Return value: KVSZP_OK (0) or a negative KVSZP_E* code.  The message of
+ *    the last failure on the calling thread is kvszp_last_error().
+ *  - Pointer arrays (page lists) live in HOST memory; the pointers in them
+ *    are DEVICE addresses.  Layer-index arrays are DEVICE int64 arrays, as in
+ *    the reference (a torch cuda int64 tensor).
+ *  - `stream` is a hipStream_t (0 = legacy default stream).  Compress entry
+ *    points block until sizes are on the host (the reference synchronizes,
+ *    cuszp_wrapper.cpp:530); decompress entry points only enqueue
+ *    (cuszp_wrapper.cpp:1102-1109).
+ *  - A context owns grow-only device workspaces, so one context must not be
+ *    used from two host threads or two streams at once (same as the
+ *    reference's CuSZpWrapper).
+ *  - Compressed streams are byte-exact to the reference fixed-mode layout:
+ *    R = 1024*ceil(N/32768) header bytes (one rate byte per 32-element
+ *    block, padding written as 0), then per block with rate r > 0 a sign
+ *    word and r bit-plane words.  Compressed buffers must be 4-byte aligned
+ *    (the reference stores uchar4 words, cuszp_batched_fixed.cu:326).
+ */
+#ifndef KVSZP_H
+#define KVSZP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct kvszp_ctx kvszp_ctx;
+typedef void* kvszp_stream_t; /* hipStream_t */
+
+enum {
+    KVSZP_OK = 0,
+    KVSZP_EINVAL = -1,   /* argument validation failed (reference: false) */
+    KVSZP_EHIP = -2,     /* a HIP runtime call failed */
+    KVSZP_ENOMEM = -3,   /* workspace allocation failed */
+    KVSZP_EDEVICE = -4   /* a kernel reported an error (bad layer index,
+                            malformed stream, or a bounded wait expired) */
+};
+
+/* Mirrors cuSZp's enums as exposed by pybind11_bindings.cpp:13-28. */
+enum { KVSZP_DIM_1D = 0, KVSZP_DIM_2D = 1, KVSZP_DIM_3D = 2 };
+enum { KVSZP_MODE_FIXED = 0, KVSZP_MODE_PLAIN = 1, KVSZP_MODE_OUTLIER = 2 };
+enum { KVSZP_TYPE_FLOAT = 0, KVSZP_TYPE_DOUBLE = 1 };
+
+/* Quantizer reading of cuszp_batched_fixed.cu:17-20 (mul.f32 then add.f32
+ * without rounding modifiers): two roundings (default) or one fused FMA. */
+enum { KVSZP_QUANT_TWO_ROUNDINGS = 0, KVSZP_QUANT_FUSED = 1 };
+/* Rate-0 blocks on decode: write +0.0 (default) or leave the destination
+ * untouched exactly like the reference (cuszp_batched_fixed.cu:496). */
+enum { KVSZP_RATE0_SKIP = 0, KVSZP_RATE0_ZERO = 1 };
+
+/* CuSZpWrapper::CompressionConfig, cuszp_wrapper.h:11-17. */
+typedef struct kvszp_config {
+    float error_bound;      /* default 1e-4 */
+    int use_relative_error; /* default 1 */
+    int processing_dim;     /* KVSZP_DIM_* (default 1D) */
+    int encoding_mode;      /* KVSZP_MODE_* (default PLAIN) */
+    int data_type;          /* KVSZP_TYPE_* (default FLOAT) */
+} kvszp_config;
+
+/* Replaces CuSZpWrapper(config, device_id), cuszp_wrapper.cpp:23-39. */
+int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out);
+/* Replaces ~CuSZpWrapper, cuszp_wrapper.cpp:41-66. */
+int kvszp_destroy(kvszp_ctx* ctx);
+/* Replaces get_config / update_config, cuszp_wrapper.h:126-127. */
+int kvszp_get_config(const kvszp_ctx* ctx, kvszp_config* out);
+int kvszp_update_config(kvszp_ctx* ctx, const kvszp_config* config);
+/* Codec options with no reference counterpart (see the enums above). */
+int kvszp_set_options(kvszp_ctx* ctx, int quantizer, int rate0_policy);
+
+/* Replaces CuSZpWrapper::estimate_compressed_buffer_size,
+ * cuszp_wrapper.cpp:1319-1321 (2 x bytes; callers pass 4*N). */
+size_t kvszp_estimate_compressed_buffer_size(size_t original_size);
+/* Header bytes R of a stream of n elements (cuszp_wrapper.cpp:534-535). */
+size_t kvszp_header_bytes(size_t num_elements);
+
+/* Replaces CuSZpWrapper::compress_batch_fixed_bf16,
+ * cuszp_wrapper.cpp:431-544 (binding pybind11_bindings.cpp:84-101).
+ *  inputs[batch]      : device BF16 pages, num_elements each
+ *  outputs[batch]     : device byte buffers, capacities[i] bytes each
+ *                       (must be >= 8*num_elements, cuszp_wrapper.cpp:449)
+ *  eps_overrides      : NULL or [batch]; eps_i > 0 overrides error_bound
+ *  sizes_out[batch]   : stream bytes S_i
+ *  bounds_out[batch]  : absolute error bound used for page i */
+int kvszp_compress_batch_fixed_bf16(
+    kvszp_ctx* ctx, const void* const* inputs, void* const* outputs,
+    const uint64_t* capacities, const float* eps_overrides, size_t batch,
+    size_t num_elements, kvszp_stream_t stream, uint64_t* sizes_out,
+    float* bounds_out);
+
+/* Replaces CuSZpWrapper::compress_batch_fixed_bf16_indexed,
+ * cuszp_wrapper.cpp:548-681 (pybind11_bindings.cpp:104-132).  Page i is
+ * read as view(prefix_count, source_layers, elements_per_layer) and the
+ * layers in layer_indices[selected_layers] (device int64) are encoded as one
+ * logical segment of prefix_count*selected_layers*elements_per_layer values. */
+int kvszp_compress_batch_fixed_bf16_indexed(
+    kvszp_ctx* ctx, const void* const* inputs, void* const* outputs,
+    const uint64_t* capacities, const int64_t* layer_indices,
+    size_t selected_layers, size_t prefix_count, size_t source_layers,
+    size_t elements_per_layer, const float* eps_overrides, size_t batch,
+    kvszp_stream_t stream, uint64_t* sizes_out, float* bounds_out);
+
+/* Replaces CuSZpWrapper::compress_batch_fixed_bf16_indexed_groups,
+ * cuszp_wrapper.cpp:683-868 (pybind11_bindings.cpp:133-163).  Requests are
+ * laid out group by group: group g covers the next group_sizes[g] entries of
+ * inputs/outputs and uses layer_indices[g] (device int64, selected_layers[g]
+ * long).  All groups run in ONE kernel launch (the reference launches once
+ * per group). */
+int kvszp_compress_batch_fixed_bf16_indexed_groups(
+    kvszp_ctx* ctx, const void* const* inputs, void* const* outputs,
+    const uint64_t* capacities, const int64_t* const* layer_indices,
+    const size_t* selected_layers, const size_t* group_sizes,
+    size_t num_groups, size_t prefix_count, size_t source_layers,
+    size_t elements_per_layer, const float* eps_overrides, size_t batch,
+    kvszp_stream_t stream, uint64_t* sizes_out, float* bounds_out);
+
+/* Replaces CuSZpWrapper::decompress_batch_fixed_bf16,
+ * cuszp_wrapper.cpp:1034-1110 (pybind11_bindings.cpp:190-207).  Page i is
+ * decoded to output + i*num_elements_per_page; output holds
+ * output_elements >= batch*num_elements_per_page BF16 values. */
+int kvszp_decompress_batch_fixed_bf16(
+    kvszp_ctx* ctx, const void* const* compressed, const uint64_t* sizes,
+    const float* error_bounds, size_t batch, void* output,
+    size_t output_elements, size_t num_elements_per_page,
+    kvszp_stream_t stream);
+
+/* Replaces CuSZpWrapper::decompress_batch_fixed_bf16_scatter,
+ * cuszp_wrapper.cpp:1111-1212 (pybind11_bindings.cpp:208-230).  Logical
+ * element e of page i goes to
+ *   destinations[i*destinations_per_page + e/elements_per_destination]
+ *               [e % elements_per_destination];
+ * num_elements_per_page == destinations_per_page*elements_per_destination. */
+int kvszp_decompress_batch_fixed_bf16_scatter(
+    kvszp_ctx* ctx, const void* const* compressed, const uint64_t* sizes,
+    const float* error_bounds, size_t batch, void* const* destinations,
+    size_t num_elements_per_page, size_t destinations_per_page,
+    size_t elements_per_destination, kvszp_stream_t stream);
+
+/* Replaces CuSZpWrapper::decompress_batch_fixed_bf16_indexed_scatter,
+ * cuszp_wrapper.cpp:1214-1313 (pybind11_bindings.cpp:232-256).  Decodes the
+ * layer-selected segment straight into the full page destinations[i]
+ * (view(prefix_count, source_layers, elements_per_layer)). */
+int kvszp_decompress_batch_fixed_bf16_indexed_scatter(
+    kvszp_ctx* ctx, const void* const* compressed, const uint64_t* sizes,
+    const float* error_bounds, size_t batch, void* const* destinations,
+    const int64_t* layer_indices, size_t selected_layers,
+    size_t prefix_count, size_t source_layers, size_t elements_per_layer,
+    kvszp_stream_t stream);
+
+/* Waits for `stream` and reports any error a kernel of this context flagged
+ * since the last check (decompress calls only enqueue, so their device-side
+ * errors surface here or at the next compress call).  No reference
+ * counterpart: the reference's decoders have no device-side checks. */
+int kvszp_synchronize(kvszp_ctx* ctx, kvszp_stream_t stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* kvszp_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVSZP_H */

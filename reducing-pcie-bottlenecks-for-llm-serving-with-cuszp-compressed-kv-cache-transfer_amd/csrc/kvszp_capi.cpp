@@ -1,0 +1,732 @@
+// kvszp_capi.cpp -- host side of the C ABI declared in include/kvszp.h.
+//
+// Replaces the batched BF16 methods of CuSZpWrapper
+// (integration/cuszp_wrapper/cuszp_wrapper.cpp:431-868, 1034-1313).
+// Differences in mechanism (not in results):
+//  - one launch per call, also for grouped requests (the reference launches
+//    once per group, cuszp_wrapper.cpp:795-848);
+//  - no per-call memsets: cross-workgroup words carry an epoch tag;
+//  - one H2D copy of a packed job table from a pinned staging ring, and one
+//    D2H copy of all sizes (the reference issues one D2H per page,
+//    cuszp_wrapper.cpp:523-529).
+#include "kvszp.h"
+#include "kvszp_internal.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace kvszp;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(KVSZP_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+struct DevBuf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct StagingSlot {
+    void* host = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+};
+
+constexpr int kSlots = 4;
+constexpr uint32_t kEpochLimit = (1u << 30) - 2u;
+constexpr uint64_t kMaxElements = 1ull << 29;      // per logical segment
+constexpr uint64_t kMaxTiles = (1ull << 32) / kThreads - 1;
+
+struct GroupSpec {
+    uint64_t n;
+    const int64_t* layers;
+    uint64_t sel, src, epl;
+    uint32_t jobs;
+};
+
+}  // namespace
+
+struct kvszp_ctx {
+    kvszp_config config;
+    int device = 0;
+    int quantizer = KVSZP_QUANT_TWO_ROUNDINGS;
+    int rate0 = KVSZP_RATE0_ZERO;
+    uint32_t fused_tile_limit = 0;
+    // control words: [0] ticket counter, [1] low 32 bits = error word
+    unsigned long long* control = nullptr;
+    unsigned long long ticket_next = 0;
+    uint32_t epoch = 0;
+    DevBuf tile_state, tile_minmax, job_minmax, tables, results;
+    StagingSlot slots[kSlots];
+    int next_slot = 0;
+    void* host_results = nullptr;
+    size_t host_results_bytes = 0;
+};
+
+namespace {
+
+uint32_t* error_word(kvszp_ctx* c) {
+    return reinterpret_cast<uint32_t*>(c->control + 1);
+}
+
+int use_device(kvszp_ctx* c) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (cur != c->device) {
+        e = hipSetDevice(c->device);
+        if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    }
+    return KVSZP_OK;
+}
+
+// Grow-only device buffer.  New memory is zeroed when `zero` (epoch-tagged
+// words must never start with a tag that could match).
+int ensure(DevBuf& b, size_t bytes, bool zero, hipStream_t stream) {
+    if (bytes <= b.bytes) return KVSZP_OK;
+    const size_t grown = std::max(bytes, b.bytes + b.bytes / 2);
+    if (b.ptr) {
+        hipError_t e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        (void)hipFree(b.ptr);
+        b.ptr = nullptr;
+        b.bytes = 0;
+    }
+    hipError_t e = hipMalloc(&b.ptr, grown);
+    if (e != hipSuccess) {
+        b.ptr = nullptr;
+        return fail(KVSZP_ENOMEM, "hipMalloc(%zu): %s", grown,
+                    hipGetErrorString(e));
+    }
+    b.bytes = grown;
+    if (zero) {
+        e = hipMemsetAsync(b.ptr, 0, grown, stream);
+        if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync");
+    }
+    return KVSZP_OK;
+}
+
+int ensure_host_results(kvszp_ctx* c, size_t bytes) {
+    if (bytes <= c->host_results_bytes) return KVSZP_OK;
+    if (c->host_results) (void)hipHostFree(c->host_results);
+    c->host_results = nullptr;
+    c->host_results_bytes = 0;
+    const size_t grown = std::max<size_t>(bytes, 4096);
+    hipError_t e = hipHostMalloc(&c->host_results, grown, hipHostMallocDefault);
+    if (e != hipSuccess) return fail(KVSZP_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
+    c->host_results_bytes = grown;
+    return KVSZP_OK;
+}
+
+// Copies `bytes` of host data to c->tables through a pinned staging slot.
+int upload_tables(kvszp_ctx* c, const void* data, size_t bytes,
+                  hipStream_t stream) {
+    int rc = ensure(c->tables, bytes, false, stream);
+    if (rc) return rc;
+    StagingSlot& s = c->slots[c->next_slot];
+    c->next_slot = (c->next_slot + 1) % kSlots;
+    hipError_t e;
+    if (s.pending) {
+        e = hipEventSynchronize(s.done);
+        if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+        s.pending = false;
+    }
+    if (bytes > s.bytes) {
+        if (s.host) (void)hipHostFree(s.host);
+        s.host = nullptr;
+        s.bytes = 0;
+        const size_t grown = std::max<size_t>(bytes, 16384);
+        e = hipHostMalloc(&s.host, grown, hipHostMallocDefault);
+        if (e != hipSuccess)
+            return fail(KVSZP_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
+        s.bytes = grown;
+    }
+    std::memcpy(s.host, data, bytes);
+    e = hipMemcpyAsync(c->tables.ptr, s.host, bytes, hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D tables)");
+    e = hipEventRecord(s.done, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+    s.pending = true;
+    return KVSZP_OK;
+}
+
+// Next epoch tag; on wrap-around all tagged words are cleared first.
+int next_epoch(kvszp_ctx* c, hipStream_t stream, uint32_t* epoch) {
+    if (c->epoch >= kEpochLimit) {
+        DevBuf* bufs[3] = {&c->tile_state, &c->tile_minmax, &c->job_minmax};
+        for (DevBuf* b : bufs) {
+            if (!b->ptr) continue;
+            hipError_t e = hipMemsetAsync(b->ptr, 0, b->bytes, stream);
+            if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync");
+        }
+        c->epoch = 0;
+    }
+    *epoch = ++c->epoch;
+    return KVSZP_OK;
+}
+
+int check_fixed_config(const kvszp_ctx* c) {
+    // cuszp_wrapper.cpp:439-446: the batched BF16 methods require fixed mode,
+    // 1D processing and the float data type.
+    if (c->config.processing_dim != KVSZP_DIM_1D ||
+        c->config.data_type != KVSZP_TYPE_FLOAT ||
+        c->config.encoding_mode != KVSZP_MODE_FIXED)
+        return fail(KVSZP_EINVAL,
+                    "batched BF16 codec requires MODE_FIXED, DIM_1D, TYPE_FLOAT");
+    return KVSZP_OK;
+}
+
+uint32_t header_bytes_of(uint64_t n) {
+    return (uint32_t)((n + kRefTileElems - 1) / kRefTileElems *
+                      (kRefTileElems / kBlockElems));
+}
+
+// Reads (and clears) the device error word.  Caller has synchronized.
+int consume_device_error(kvszp_ctx* c, uint32_t err, hipStream_t stream) {
+    if (!err) return KVSZP_OK;
+    (void)hipMemsetAsync(error_word(c), 0, sizeof(uint32_t), stream);
+    std::string what;
+    if (err & kErrSpin) what += " bounded-wait-expired";
+    if (err & kErrLayerIndex) what += " layer-index-out-of-range";
+    if (err & kErrRate) what += " rate-byte>31";
+    if (err & kErrTruncated) what += " payload-past-stream-size";
+    return fail(KVSZP_EDEVICE, "kernel reported:%s", what.c_str());
+}
+
+int validate_layers(const int64_t* layers, uint64_t sel, uint64_t prefix,
+                    uint64_t src, uint64_t epl) {
+    // cuszp_wrapper.cpp:562-575.
+    if (layers == nullptr || prefix == 0 || src == 0 || epl == 0 || sel == 0 ||
+        sel > src)
+        return fail(KVSZP_EINVAL,
+                    "invalid layer selection (prefix=%llu source_layers=%llu "
+                    "elements_per_layer=%llu selected=%llu)",
+                    (unsigned long long)prefix, (unsigned long long)src,
+                    (unsigned long long)epl, (unsigned long long)sel);
+    if (sel * epl > 0xFFFFFFFFull - kTileElems)
+        return fail(KVSZP_EINVAL, "selected layers x elements_per_layer too large");
+    return KVSZP_OK;
+}
+
+// Common compress path: `specs` are the groups, requests laid out group by
+// group in inputs/outputs.
+int compress_groups(kvszp_ctx* c, const void* const* inputs,
+                    void* const* outputs, const uint64_t* capacities,
+                    const float* eps_overrides, size_t batch,
+                    const std::vector<GroupSpec>& specs, hipStream_t stream,
+                    uint64_t* sizes_out, float* bounds_out) {
+    int rc = check_fixed_config(c);
+    if (rc) return rc;
+    if (batch == 0) return fail(KVSZP_EINVAL, "empty batch");
+    if (!inputs || !outputs || !sizes_out || !bounds_out)
+        return fail(KVSZP_EINVAL, "null pointer argument");
+    if (specs.empty() || specs.size() > (size_t)kMaxGroups)
+        return fail(KVSZP_EINVAL, "between 1 and %d groups supported", kMaxGroups);
+    rc = use_device(c);
+    if (rc) return rc;
+
+    CompressParams p;
+    std::memset(&p, 0, sizeof(p));
+    std::vector<CompressJob> jobs(batch);
+    bool aligned16 = true;
+    uint64_t total_tiles = 0;
+    uint32_t max_tiles_per_job = 0;
+    size_t job = 0;
+    for (size_t gi = 0; gi < specs.size(); ++gi) {
+        const GroupSpec& s = specs[gi];
+        if (s.n == 0 || s.n > kMaxElements)
+            return fail(KVSZP_EINVAL, "segment of %llu elements unsupported",
+                        (unsigned long long)s.n);
+        Group& g = p.groups[gi];
+        g.n = s.n;
+        g.layers = s.layers;
+        g.selected_layers = s.sel;
+        g.source_layers = s.src;
+        g.elements_per_layer = s.epl;
+        g.first_job = (uint32_t)job;
+        g.first_tile = (uint32_t)total_tiles;
+        g.tiles_per_job = (uint32_t)((s.n + kTileElems - 1) / kTileElems);
+        g.header_bytes = header_bytes_of(s.n);
+        max_tiles_per_job = std::max(max_tiles_per_job, g.tiles_per_job);
+        total_tiles += (uint64_t)g.tiles_per_job * s.jobs;
+        if (s.layers && (s.epl % 8) != 0) aligned16 = false;
+        // cuszp_wrapper.cpp:449-450 asks for capacity >= estimate(4n) = 8n.
+        // That does not cover the header of tiny segments (R = 1024 bytes for
+        // n < 128), so the worst-case stream R + 128 * nb is required too.
+        const uint64_t worst = g.header_bytes + 128ull * ((s.n + 31) / 32);
+        const uint64_t need = std::max<uint64_t>(8ull * s.n, worst);
+        for (uint32_t k = 0; k < s.jobs; ++k, ++job) {
+            if (job >= batch) return fail(KVSZP_EINVAL, "group sizes exceed batch");
+            const uintptr_t in = (uintptr_t)inputs[job];
+            const uintptr_t out = (uintptr_t)outputs[job];
+            if (!in || !out) return fail(KVSZP_EINVAL, "null page pointer %zu", job);
+            if (in & 1u) return fail(KVSZP_EINVAL, "input %zu not 2-byte aligned", job);
+            if (out & 3u)
+                return fail(KVSZP_EINVAL, "compressed buffer %zu not 4-byte aligned", job);
+            if (capacities && capacities[job] < need)
+                return fail(KVSZP_EINVAL,
+                            "compressed buffer %zu holds %llu bytes, needs %llu", job,
+                            (unsigned long long)capacities[job],
+                            (unsigned long long)need);
+            if (in & 15u) aligned16 = false;
+            const float e = (eps_overrides && eps_overrides[job] > 0.0f)
+                                ? eps_overrides[job]
+                                : c->config.error_bound;  // cuszp_wrapper.cpp:473-479
+            jobs[job].in = reinterpret_cast<const uint16_t*>(in);
+            jobs[job].out = reinterpret_cast<uint8_t*>(out);
+            jobs[job].eps = e;
+            jobs[job].reserved = 0;
+        }
+    }
+    if (job != batch) return fail(KVSZP_EINVAL, "group sizes do not cover the batch");
+    if (total_tiles == 0 || total_tiles > kMaxTiles)
+        return fail(KVSZP_EINVAL, "batch too large for one launch");
+
+    const bool relative = c->config.use_relative_error != 0;
+    int bound_mode = kBoundAbsolute;
+    if (relative)
+        bound_mode = (max_tiles_per_job <= c->fused_tile_limit) ? kBoundFused
+                                                                : kBoundPrepass;
+
+    // Workspaces.
+    if ((rc = ensure(c->tile_state, total_tiles * 8, true, stream)) ||
+        (rc = ensure(c->tile_minmax, total_tiles * 8, true, stream)) ||
+        (rc = ensure(c->job_minmax, batch * 16, true, stream)) ||
+        (rc = ensure(c->results, batch * 8, false, stream)) ||
+        (rc = ensure_host_results(c, batch * 8 + 16)))
+        return rc;
+    rc = upload_tables(c, jobs.data(), batch * sizeof(CompressJob), stream);
+    if (rc) return rc;
+    uint32_t epoch;
+    if ((rc = next_epoch(c, stream, &epoch))) return rc;
+
+    uint32_t* job_size = reinterpret_cast<uint32_t*>(c->results.ptr);
+    float* job_eb = reinterpret_cast<float*>(job_size + batch);
+    const CompressJob* djobs = reinterpret_cast<const CompressJob*>(c->tables.ptr);
+
+    hipError_t e;
+    if (bound_mode == kBoundPrepass) {
+        MinMaxParams m;
+        std::memset(&m, 0, sizeof(m));
+        m.jobs = djobs;
+        m.job_minmax = reinterpret_cast<unsigned long long*>(c->job_minmax.ptr);
+        m.error = error_word(c);
+        m.epoch = epoch;
+        m.num_groups = (int)specs.size();
+        std::memcpy(m.groups, p.groups, sizeof(m.groups));
+        e = launch_minmax(m, (uint32_t)total_tiles, stream);
+        if (e != hipSuccess) return hip_fail(e, "minmax launch");
+    }
+    p.jobs = djobs;
+    p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
+    p.tile_minmax = reinterpret_cast<unsigned long long*>(c->tile_minmax.ptr);
+    p.job_minmax = reinterpret_cast<const unsigned long long*>(c->job_minmax.ptr);
+    p.job_size = job_size;
+    p.job_eb = job_eb;
+    p.error = error_word(c);
+    p.ticket = c->control;
+    p.ticket_base = c->ticket_next;
+    p.epoch = epoch;
+    p.total_tiles = (uint32_t)total_tiles;
+    p.num_groups = (int)specs.size();
+    p.bound_mode = bound_mode;
+    p.quantizer = c->quantizer;
+    p.aligned16 = aligned16 ? 1 : 0;
+    e = launch_compress(p, stream);
+    if (e != hipSuccess) return hip_fail(e, "compress launch");
+    c->ticket_next += total_tiles;
+
+    // One D2H of sizes (+ bounds) and the error word, then wait: callers need
+    // the sizes on the host (cuszp_wrapper.cpp:520-532).
+    char* host = reinterpret_cast<char*>(c->host_results);
+    const size_t result_bytes = batch * (relative ? 8 : 4);
+    e = hipMemcpyAsync(host + 16, c->results.ptr, result_bytes,
+                       hipMemcpyDeviceToHost, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(D2H sizes)");
+    e = hipMemcpyAsync(host, error_word(c), sizeof(uint32_t),
+                       hipMemcpyDeviceToHost, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(D2H error)");
+    e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    uint32_t err;
+    std::memcpy(&err, host, sizeof(err));
+    rc = consume_device_error(c, err, stream);
+    if (rc) return rc;
+    const uint32_t* hs = reinterpret_cast<const uint32_t*>(host + 16);
+    const float* hb = reinterpret_cast<const float*>(hs + batch);
+    for (size_t i = 0; i < batch; ++i) {
+        sizes_out[i] = hs[i];
+        bounds_out[i] = relative ? hb[i] : jobs[i].eps;
+    }
+    return KVSZP_OK;
+}
+
+// Common decompress path.
+int decompress_groups(kvszp_ctx* c, const void* const* compressed,
+                      const uint64_t* sizes, const float* bounds, size_t batch,
+                      const GroupSpec& spec, int dst_kind,
+                      const std::vector<uint16_t*>& dst_base,
+                      const std::vector<uint16_t*>& dest_table, uint64_t dpp,
+                      uint64_t epd, bool aligned16, hipStream_t stream) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (spec.n == 0 || spec.n > kMaxElements)
+        return fail(KVSZP_EINVAL, "segment of %llu elements unsupported",
+                    (unsigned long long)spec.n);
+    const uint32_t R = header_bytes_of(spec.n);
+    std::vector<DecompressJob> jobs(batch);
+    for (size_t i = 0; i < batch; ++i) {
+        const uintptr_t in = (uintptr_t)compressed[i];
+        // cuszp_wrapper.cpp:1077: a zero size is rejected.  A stream shorter
+        // than its own header cannot be decoded either.
+        if (!in || sizes[i] == 0)
+            return fail(KVSZP_EINVAL, "invalid compressed page %zu", i);
+        if (sizes[i] < R)
+            return fail(KVSZP_EINVAL, "stream %zu (%llu bytes) shorter than its "
+                        "%u-byte header", i, (unsigned long long)sizes[i], R);
+        if (sizes[i] > 0xFFFFFFFFull)
+            return fail(KVSZP_EINVAL, "stream %zu too large", i);
+        if (in & 3u)
+            return fail(KVSZP_EINVAL, "compressed buffer %zu not 4-byte aligned", i);
+        jobs[i].in = reinterpret_cast<const uint8_t*>(in);
+        jobs[i].dst = dst_kind == kDstMulti ? nullptr : dst_base[i];
+        jobs[i].eb = bounds[i];
+        jobs[i].size = (uint32_t)sizes[i];
+    }
+    const uint32_t tiles_per_job = (uint32_t)((spec.n + kTileElems - 1) / kTileElems);
+    const uint64_t total_tiles = (uint64_t)tiles_per_job * batch;
+    if (total_tiles > kMaxTiles) return fail(KVSZP_EINVAL, "batch too large for one launch");
+
+    // Packed table: jobs, then (kDstMulti) the destination pointers.
+    const size_t jobs_bytes = (batch * sizeof(DecompressJob) + 255) & ~(size_t)255;
+    std::vector<char> table(jobs_bytes + dest_table.size() * sizeof(uint16_t*));
+    std::memcpy(table.data(), jobs.data(), batch * sizeof(DecompressJob));
+    if (!dest_table.empty())
+        std::memcpy(table.data() + jobs_bytes, dest_table.data(),
+                    dest_table.size() * sizeof(uint16_t*));
+    if ((rc = ensure(c->tile_state, total_tiles * 8, true, stream))) return rc;
+    if ((rc = upload_tables(c, table.data(), table.size(), stream))) return rc;
+    uint32_t epoch;
+    if ((rc = next_epoch(c, stream, &epoch))) return rc;
+
+    DecompressParams p;
+    std::memset(&p, 0, sizeof(p));
+    p.jobs = reinterpret_cast<const DecompressJob*>(c->tables.ptr);
+    p.dests = reinterpret_cast<uint16_t* const*>(
+        reinterpret_cast<char*>(c->tables.ptr) + jobs_bytes);
+    p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
+    p.error = error_word(c);
+    p.ticket = c->control;
+    p.ticket_base = c->ticket_next;
+    p.epoch = epoch;
+    p.total_tiles = (uint32_t)total_tiles;
+    p.num_groups = 1;
+    p.dst_kind = dst_kind;
+    p.rate0_zero = c->rate0 == KVSZP_RATE0_ZERO ? 1 : 0;
+    p.aligned16 = aligned16 ? 1 : 0;
+    p.dests_per_page = dpp;
+    p.elements_per_dest = epd;
+    Group& g = p.groups[0];
+    g.n = spec.n;
+    g.layers = spec.layers;
+    g.selected_layers = spec.sel;
+    g.source_layers = spec.src;
+    g.elements_per_layer = spec.epl;
+    g.first_job = 0;
+    g.first_tile = 0;
+    g.tiles_per_job = tiles_per_job;
+    g.header_bytes = R;
+    hipError_t e = launch_decompress(p, stream);
+    if (e != hipSuccess) return hip_fail(e, "decompress launch");
+    c->ticket_next += total_tiles;
+    return KVSZP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
+    if (!out) return fail(KVSZP_EINVAL, "null output handle");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device_id < 0 || device_id >= count)
+        return fail(KVSZP_EINVAL, "device %d not present (%d devices)", device_id, count);
+    e = hipSetDevice(device_id);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    kvszp_ctx* c = new kvszp_ctx();
+    if (config) {
+        c->config = *config;
+    } else {  // CompressionConfig defaults, cuszp_wrapper.h:11-17
+        c->config.error_bound = 1e-4f;
+        c->config.use_relative_error = 1;
+        c->config.processing_dim = KVSZP_DIM_1D;
+        c->config.encoding_mode = KVSZP_MODE_PLAIN;
+        c->config.data_type = KVSZP_TYPE_FLOAT;
+    }
+    c->device = device_id;
+    e = hipMalloc(&c->control, 64);
+    if (e == hipSuccess) e = hipMemset(c->control, 0, 64);
+    for (int i = 0; e == hipSuccess && i < kSlots; ++i)
+        e = hipEventCreateWithFlags(&c->slots[i].done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        kvszp_destroy(c);
+        return hip_fail(e, "context setup");
+    }
+    // Tiles of one job wait for each other in the fused relative-bound
+    // exchange, so a job may use it only if all its tiles fit on the device
+    // at once with a wide margin.
+    const int resident = compress_resident_workgroups(device_id);
+    c->fused_tile_limit = (uint32_t)std::min(kThreads, std::max(0, resident / 4));
+    *out = c;
+    return KVSZP_OK;
+}
+
+int kvszp_destroy(kvszp_ctx* c) {
+    if (!c) return KVSZP_OK;
+    (void)hipSetDevice(c->device);
+    for (auto& s : c->slots) {
+        if (s.done) {
+            if (s.pending) (void)hipEventSynchronize(s.done);
+            (void)hipEventDestroy(s.done);
+        }
+        if (s.host) (void)hipHostFree(s.host);
+    }
+    DevBuf* bufs[5] = {&c->tile_state, &c->tile_minmax, &c->job_minmax,
+                       &c->tables, &c->results};
+    for (DevBuf* b : bufs)
+        if (b->ptr) (void)hipFree(b->ptr);
+    if (c->control) (void)hipFree(c->control);
+    if (c->host_results) (void)hipHostFree(c->host_results);
+    delete c;
+    return KVSZP_OK;
+}
+
+int kvszp_get_config(const kvszp_ctx* c, kvszp_config* out) {
+    if (!c || !out) return fail(KVSZP_EINVAL, "null argument");
+    *out = c->config;
+    return KVSZP_OK;
+}
+
+int kvszp_update_config(kvszp_ctx* c, const kvszp_config* config) {
+    if (!c || !config) return fail(KVSZP_EINVAL, "null argument");
+    c->config = *config;
+    return KVSZP_OK;
+}
+
+int kvszp_set_options(kvszp_ctx* c, int quantizer, int rate0_policy) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (quantizer != KVSZP_QUANT_TWO_ROUNDINGS && quantizer != KVSZP_QUANT_FUSED)
+        return fail(KVSZP_EINVAL, "unknown quantizer %d", quantizer);
+    if (rate0_policy != KVSZP_RATE0_SKIP && rate0_policy != KVSZP_RATE0_ZERO)
+        return fail(KVSZP_EINVAL, "unknown rate-0 policy %d", rate0_policy);
+    c->quantizer = quantizer;
+    c->rate0 = rate0_policy;
+    return KVSZP_OK;
+}
+
+size_t kvszp_estimate_compressed_buffer_size(size_t original_size) {
+    return original_size * 2;
+}
+
+size_t kvszp_header_bytes(size_t num_elements) { return header_bytes_of(num_elements); }
+
+int kvszp_compress_batch_fixed_bf16(kvszp_ctx* c, const void* const* inputs,
+                                    void* const* outputs,
+                                    const uint64_t* capacities,
+                                    const float* eps_overrides, size_t batch,
+                                    size_t num_elements, kvszp_stream_t stream,
+                                    uint64_t* sizes_out, float* bounds_out) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    std::vector<GroupSpec> specs(1);
+    specs[0] = GroupSpec{num_elements, nullptr, 0, 0, 0, (uint32_t)batch};
+    return compress_groups(c, inputs, outputs, capacities, eps_overrides, batch,
+                           specs, (hipStream_t)stream, sizes_out, bounds_out);
+}
+
+int kvszp_compress_batch_fixed_bf16_indexed(
+    kvszp_ctx* c, const void* const* inputs, void* const* outputs,
+    const uint64_t* capacities, const int64_t* layer_indices,
+    size_t selected_layers, size_t prefix_count, size_t source_layers,
+    size_t elements_per_layer, const float* eps_overrides, size_t batch,
+    kvszp_stream_t stream, uint64_t* sizes_out, float* bounds_out) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    int rc = validate_layers(layer_indices, selected_layers, prefix_count,
+                             source_layers, elements_per_layer);
+    if (rc) return rc;
+    std::vector<GroupSpec> specs(1);
+    specs[0] = GroupSpec{(uint64_t)prefix_count * selected_layers * elements_per_layer,
+                         layer_indices, selected_layers, source_layers,
+                         elements_per_layer, (uint32_t)batch};
+    return compress_groups(c, inputs, outputs, capacities, eps_overrides, batch,
+                           specs, (hipStream_t)stream, sizes_out, bounds_out);
+}
+
+int kvszp_compress_batch_fixed_bf16_indexed_groups(
+    kvszp_ctx* c, const void* const* inputs, void* const* outputs,
+    const uint64_t* capacities, const int64_t* const* layer_indices,
+    const size_t* selected_layers, const size_t* group_sizes,
+    size_t num_groups, size_t prefix_count, size_t source_layers,
+    size_t elements_per_layer, const float* eps_overrides, size_t batch,
+    kvszp_stream_t stream, uint64_t* sizes_out, float* bounds_out) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (num_groups == 0 || !layer_indices || !selected_layers || !group_sizes)
+        return fail(KVSZP_EINVAL, "empty group list");
+    std::vector<GroupSpec> specs;
+    uint64_t covered = 0;
+    for (size_t gi = 0; gi < num_groups; ++gi) {
+        // cuszp_wrapper.cpp:717-743.
+        if (group_sizes[gi] == 0)
+            return fail(KVSZP_EINVAL, "group %zu is empty", gi);
+        int rc = validate_layers(layer_indices[gi], selected_layers[gi],
+                                 prefix_count, source_layers, elements_per_layer);
+        if (rc) return rc;
+        specs.push_back(GroupSpec{
+            (uint64_t)prefix_count * selected_layers[gi] * elements_per_layer,
+            layer_indices[gi], selected_layers[gi], source_layers,
+            elements_per_layer, (uint32_t)group_sizes[gi]});
+        covered += group_sizes[gi];
+    }
+    if (covered != batch)
+        return fail(KVSZP_EINVAL, "group sizes sum to %llu, batch is %zu",
+                    (unsigned long long)covered, batch);
+    return compress_groups(c, inputs, outputs, capacities, eps_overrides, batch,
+                           specs, (hipStream_t)stream, sizes_out, bounds_out);
+}
+
+int kvszp_decompress_batch_fixed_bf16(kvszp_ctx* c, const void* const* compressed,
+                                      const uint64_t* sizes,
+                                      const float* error_bounds, size_t batch,
+                                      void* output, size_t output_elements,
+                                      size_t num_elements_per_page,
+                                      kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (batch == 0) return KVSZP_OK;  // cuszp_wrapper.cpp:1042
+    int rc = check_fixed_config(c);
+    if (rc) return rc;
+    if (!compressed || !sizes || !error_bounds || !output ||
+        num_elements_per_page == 0 ||
+        output_elements < batch * num_elements_per_page)
+        return fail(KVSZP_EINVAL, "invalid fixed BF16 batch metadata");
+    if ((uintptr_t)output & 1u) return fail(KVSZP_EINVAL, "output not 2-byte aligned");
+    std::vector<uint16_t*> base(batch);
+    for (size_t i = 0; i < batch; ++i)
+        base[i] = reinterpret_cast<uint16_t*>(output) + i * num_elements_per_page;
+    const bool aligned16 =
+        ((uintptr_t)output & 15u) == 0 && (num_elements_per_page % 8) == 0;
+    GroupSpec spec{num_elements_per_page, nullptr, 0, 0, 0, (uint32_t)batch};
+    return decompress_groups(c, compressed, sizes, error_bounds, batch, spec,
+                             kDstLinear, base, {}, 0, 0, aligned16,
+                             (hipStream_t)stream);
+}
+
+int kvszp_decompress_batch_fixed_bf16_scatter(
+    kvszp_ctx* c, const void* const* compressed, const uint64_t* sizes,
+    const float* error_bounds, size_t batch, void* const* destinations,
+    size_t num_elements_per_page, size_t destinations_per_page,
+    size_t elements_per_destination, kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (batch == 0) return KVSZP_OK;  // cuszp_wrapper.cpp:1121
+    int rc = check_fixed_config(c);
+    if (rc) return rc;
+    // cuszp_wrapper.cpp:1123-1133.
+    if (!compressed || !sizes || !error_bounds || !destinations ||
+        destinations_per_page == 0 || elements_per_destination == 0 ||
+        num_elements_per_page != destinations_per_page * elements_per_destination)
+        return fail(KVSZP_EINVAL, "invalid direct-scatter metadata");
+    const size_t count = batch * destinations_per_page;
+    std::vector<uint16_t*> dests(count);
+    bool aligned16 = true;
+    for (size_t i = 0; i < count; ++i) {
+        const uintptr_t d = (uintptr_t)destinations[i];
+        if (!d || (d & 1u))
+            return fail(KVSZP_EINVAL, "invalid BF16 direct-scatter destination %zu", i);
+        if (d & 15u) aligned16 = false;
+        dests[i] = reinterpret_cast<uint16_t*>(d);
+    }
+    GroupSpec spec{num_elements_per_page, nullptr, 0, 0, 0, (uint32_t)batch};
+    if (destinations_per_page == 1) {
+        // One destination per page: straight 16-byte stores into the page
+        // (cu:383-386, 566-576).
+        return decompress_groups(c, compressed, sizes, error_bounds, batch, spec,
+                                 kDstLinear, dests, {}, 0, 0,
+                                 aligned16 && (num_elements_per_page % 8) == 0,
+                                 (hipStream_t)stream);
+    }
+    return decompress_groups(c, compressed, sizes, error_bounds, batch, spec,
+                             kDstMulti, {}, dests, destinations_per_page,
+                             elements_per_destination, false, (hipStream_t)stream);
+}
+
+int kvszp_decompress_batch_fixed_bf16_indexed_scatter(
+    kvszp_ctx* c, const void* const* compressed, const uint64_t* sizes,
+    const float* error_bounds, size_t batch, void* const* destinations,
+    const int64_t* layer_indices, size_t selected_layers, size_t prefix_count,
+    size_t source_layers, size_t elements_per_layer, kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (batch == 0) return KVSZP_OK;  // cuszp_wrapper.cpp:1227
+    int rc = check_fixed_config(c);
+    if (rc) return rc;
+    rc = validate_layers(layer_indices, selected_layers, prefix_count,
+                         source_layers, elements_per_layer);
+    if (rc) return rc;
+    if (!compressed || !sizes || !error_bounds || !destinations)
+        return fail(KVSZP_EINVAL, "null pointer argument");
+    std::vector<uint16_t*> dests(batch);
+    for (size_t i = 0; i < batch; ++i) {
+        const uintptr_t d = (uintptr_t)destinations[i];
+        if (!d || (d & 1u))
+            return fail(KVSZP_EINVAL, "invalid BF16 destination page %zu", i);
+        dests[i] = reinterpret_cast<uint16_t*>(d);
+    }
+    GroupSpec spec{(uint64_t)prefix_count * selected_layers * elements_per_layer,
+                   layer_indices, selected_layers, source_layers,
+                   elements_per_layer, (uint32_t)batch};
+    return decompress_groups(c, compressed, sizes, error_bounds, batch, spec,
+                             kDstIndexed, dests, {}, 0, 0, false,
+                             (hipStream_t)stream);
+}
+
+int kvszp_synchronize(kvszp_ctx* c, kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    int rc = use_device(c);
+    if (rc) return rc;
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    uint32_t err = 0;
+    e = hipMemcpy(&err, error_word(c), sizeof(err), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy(error word)");
+    rc = consume_device_error(c, err, (hipStream_t)stream);
+    if (rc) {
+        (void)hipStreamSynchronize((hipStream_t)stream);
+        return rc;
+    }
+    return KVSZP_OK;
+}
+
+const char* kvszp_last_error(void) { return g_last_error.c_str(); }
+
+}  // extern "C"

@@ -1,0 +1,134 @@
+// kvszp_internal.h -- launch descriptors shared by the HIP kernels
+// (kvszp_kernels.hip) and the host C-ABI (kvszp_capi.cpp).
+//
+// Work decomposition.  A "job" is one logical segment to encode or decode
+// (one page, or the layer-selected part of one page).  Jobs with the same
+// geometry form a "group".  Every job is cut into tiles of kTileBlocks
+// fixed-rate blocks (kTileBlocks * 32 elements); one workgroup of
+// kTileBlocks threads handles one tile, one thread per 32-element block.
+// Tiles are numbered group by group, job by job, so the tiles of a job are
+// consecutive.  Workgroups take tile numbers from a ticket counter, so a
+// tile only ever waits for tiles that already started (forward progress
+// does not depend on dispatch order).
+#ifndef KVSZP_INTERNAL_H
+#define KVSZP_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvszp {
+
+constexpr int kBlockElems = 32;                     // fixed-rate block
+constexpr int kTileBlocks = 256;                    // blocks per tile
+constexpr int kThreads = kTileBlocks;               // one thread per block
+constexpr int kTileElems = kTileBlocks * kBlockElems;
+constexpr int kRefTileElems = 32768;                // header granularity
+constexpr int kMaxGroups = 16;
+constexpr uint32_t kSpinLimit = 1u << 20;           // bounded waits (~1 s)
+
+// Device-side error bits (OR-ed into the context's error word).
+enum : uint32_t {
+    kErrSpin = 1u,         // a bounded wait expired
+    kErrLayerIndex = 2u,   // a layer index outside [0, source_layers)
+    kErrRate = 4u,         // a rate byte > 31 in a stream
+    kErrTruncated = 8u,    // payload past the declared stream size
+};
+
+// How the relative error bound is obtained.
+enum : int {
+    kBoundAbsolute = 0,    // eb = job eps
+    kBoundFused = 1,       // per-job min/max exchanged inside the kernel
+    kBoundPrepass = 2,     // per-job min/max from a preceding reduction
+};
+
+// Decoder destination kinds.
+enum : int {
+    kDstLinear = 0,        // element e -> dst + e
+    kDstMulti = 1,         // element e -> dests[job*dpp + e/epd] + e%epd
+    kDstIndexed = 2,       // element e -> dst + layer-mapped index
+};
+
+struct Group {
+    uint64_t n;                 // logical elements per job
+    const int64_t* layers;      // device layer map, nullptr = contiguous
+    uint64_t selected_layers;
+    uint64_t source_layers;
+    uint64_t elements_per_layer;
+    uint32_t first_job;
+    uint32_t first_tile;
+    uint32_t tiles_per_job;
+    uint32_t header_bytes;      // R = 1024 * ceil(n / 32768)
+};
+
+struct CompressJob {
+    const uint16_t* in;         // BF16 page (full page when indexed)
+    uint8_t* out;               // stream buffer, 4-byte aligned
+    float eps;                  // eps (relative) or eb (absolute)
+    uint32_t reserved;
+};
+
+struct DecompressJob {
+    const uint8_t* in;          // stream, 4-byte aligned
+    uint16_t* dst;              // destination base (kDstLinear/kDstIndexed)
+    float eb;                   // absolute error bound
+    uint32_t size;              // declared stream bytes (read bound)
+};
+
+struct CompressParams {
+    const CompressJob* jobs;
+    unsigned long long* tile_state;   // look-back words, one per tile
+    unsigned long long* tile_minmax;  // fused min/max words, one per tile
+    const unsigned long long* job_minmax;  // pre-pass words, two per job
+    uint32_t* job_size;               // out: stream bytes per job
+    float* job_eb;                    // out: absolute bound per job
+    uint32_t* error;
+    unsigned long long* ticket;
+    unsigned long long ticket_base;
+    uint32_t epoch;
+    uint32_t total_tiles;
+    int num_groups;
+    int bound_mode;
+    int quantizer;                    // 0 two roundings, 1 fused
+    int aligned16;                    // every input page is 16-byte aligned
+    Group groups[kMaxGroups];
+};
+
+struct MinMaxParams {
+    const CompressJob* jobs;
+    unsigned long long* job_minmax;   // two words per job: max key, ~min key
+    uint32_t* error;
+    uint32_t epoch;
+    uint32_t chunks_per_job;          // workgroups per job
+    int num_groups;
+    Group groups[kMaxGroups];         // first_tile is the first chunk
+};
+
+struct DecompressParams {
+    const DecompressJob* jobs;
+    uint16_t* const* dests;           // kDstMulti destination table
+    unsigned long long* tile_state;
+    uint32_t* error;
+    unsigned long long* ticket;
+    unsigned long long ticket_base;
+    uint32_t epoch;
+    uint32_t total_tiles;
+    int num_groups;
+    int dst_kind;
+    int rate0_zero;                   // 1: write +0.0 for rate-0 blocks
+    int aligned16;                    // every destination base 16B aligned
+    uint64_t dests_per_page;
+    uint64_t elements_per_dest;
+    Group groups[kMaxGroups];
+};
+
+// Launchers (kvszp_kernels.hip).  Return hipGetLastError() of the launch.
+hipError_t launch_compress(const CompressParams& p, hipStream_t stream);
+hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
+                         hipStream_t stream);
+hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream);
+// Maximum co-resident workgroups of the compress kernel on this device.
+int compress_resident_workgroups(int device);
+
+}  // namespace kvszp
+
+#endif  // KVSZP_INTERNAL_H

@@ -1,0 +1,481 @@
+"""Drop-in replacement for the reference's ``cuszp_wrapper_cpp`` module.
+
+The reference builds this module with pybind11 from
+``integration/cuszp_wrapper/pybind11_bindings.cpp``; its caller,
+``integration/compression_pipeline/vllm_v1_compressed_offload.py``, does
+``import cuszp_wrapper_cpp`` after putting the module's directory on
+``sys.path`` (:41-45).  Put this directory on ``sys.path`` instead and the
+connector runs on the MI355X HIP codec unchanged.
+
+Kept exactly: enum names and values (:13-28), ``CompressionConfig`` fields and
+defaults (:31-43), ``CuSZpWrapper(config, device_id=0)`` and the method
+names, argument names and order, and return shapes of the batched BF16
+fixed-mode path (:84-163, :190-256), ``estimate_compressed_buffer_size``
+(:260-261), ``get_config``/``update_config`` (:262-263).  Validation follows
+the reference's C++ checks (cuszp_wrapper.cpp:431-868, 1034-1313): a failed
+check returns ``False`` (or a ``False`` tuple) instead of raising.  Every
+call runs on ``torch.cuda.current_stream()`` (the reference captures
+``c10::cuda::getCurrentCUDAStream()`` per call); compress calls block until
+the sizes are on the host, decompress calls only enqueue.
+
+The single-page fp32 entry points (``compress``, ``compress_batch_fixed``,
+``decompress``, ``decompress_batch``) belong to the upstream cuSZp fp32
+kernels, which this codec does not implement; they report failure (the
+connector then raises or falls back, as it does on any codec failure).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+import sys
+
+import numpy as np
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+if _HERE not in sys.path:
+    sys.path.insert(0, _HERE)
+
+import kvszp  # noqa: E402  (the C ABI; raises if libkvszp.so is missing)
+
+kvszp.load()
+
+
+class CuszpDim(enum.IntEnum):
+    DIM_1D = kvszp.DIM_1D
+    DIM_2D = kvszp.DIM_2D
+    DIM_3D = kvszp.DIM_3D
+
+
+class CuszpMode(enum.IntEnum):
+    MODE_FIXED = kvszp.MODE_FIXED
+    MODE_PLAIN = kvszp.MODE_PLAIN
+    MODE_OUTLIER = kvszp.MODE_OUTLIER
+
+
+class CuszpType(enum.IntEnum):
+    TYPE_FLOAT = kvszp.TYPE_FLOAT
+    TYPE_DOUBLE = kvszp.TYPE_DOUBLE
+
+
+# pybind11's export_values() also puts the enumerators in the module scope.
+DIM_1D, DIM_2D, DIM_3D = CuszpDim.DIM_1D, CuszpDim.DIM_2D, CuszpDim.DIM_3D
+MODE_FIXED, MODE_PLAIN, MODE_OUTLIER = (
+    CuszpMode.MODE_FIXED, CuszpMode.MODE_PLAIN, CuszpMode.MODE_OUTLIER)
+TYPE_FLOAT, TYPE_DOUBLE = CuszpType.TYPE_FLOAT, CuszpType.TYPE_DOUBLE
+
+
+def _f32(value: float) -> float:
+    """Rounds a Python float through C float, as pybind11 does."""
+    return float(np.float32(value))
+
+
+class CompressionConfig:
+    """CuSZpWrapper::CompressionConfig (cuszp_wrapper.h:11-17)."""
+
+    def __init__(self, error_bound: float = 1e-4,
+                 use_relative_error: bool = True,
+                 processing_dim: CuszpDim = CuszpDim.DIM_1D,
+                 encoding_mode: CuszpMode = CuszpMode.MODE_PLAIN,
+                 data_type: CuszpType = CuszpType.TYPE_FLOAT):
+        self.error_bound = error_bound
+        self.use_relative_error = use_relative_error
+        self.processing_dim = processing_dim
+        self.encoding_mode = encoding_mode
+        self.data_type = data_type
+
+    @property
+    def error_bound(self) -> float:
+        return self._error_bound
+
+    @error_bound.setter
+    def error_bound(self, value: float) -> None:
+        self._error_bound = _f32(value)
+
+    @property
+    def use_relative_error(self) -> bool:
+        return self._use_relative_error
+
+    @use_relative_error.setter
+    def use_relative_error(self, value: bool) -> None:
+        self._use_relative_error = bool(value)
+
+    @property
+    def processing_dim(self) -> CuszpDim:
+        return self._processing_dim
+
+    @processing_dim.setter
+    def processing_dim(self, value) -> None:
+        self._processing_dim = CuszpDim(int(value))
+
+    @property
+    def encoding_mode(self) -> CuszpMode:
+        return self._encoding_mode
+
+    @encoding_mode.setter
+    def encoding_mode(self, value) -> None:
+        self._encoding_mode = CuszpMode(int(value))
+
+    @property
+    def data_type(self) -> CuszpType:
+        return self._data_type
+
+    @data_type.setter
+    def data_type(self, value) -> None:
+        self._data_type = CuszpType(int(value))
+
+    def _to_c(self) -> kvszp.Config:
+        return kvszp.Config(self.error_bound, int(self.use_relative_error),
+                            int(self.processing_dim), int(self.encoding_mode),
+                            int(self.data_type))
+
+    def _copy(self) -> "CompressionConfig":
+        return CompressionConfig(self.error_bound, self.use_relative_error,
+                                 self.processing_dim, self.encoding_mode,
+                                 self.data_type)
+
+    def __repr__(self) -> str:
+        return (f"CompressionConfig(error_bound={self.error_bound}, "
+                f"use_relative_error={self.use_relative_error}, "
+                f"processing_dim={self.processing_dim.name}, "
+                f"encoding_mode={self.encoding_mode.name}, "
+                f"data_type={self.data_type.name})")
+
+
+def _stream_handle(device_id: int) -> int:
+    return torch.cuda.current_stream(device_id).cuda_stream
+
+
+def _report(where: str) -> None:
+    # The reference prints its failures to stderr and returns false
+    # (cuszp_wrapper.cpp:11-19, cuszp_batched_fixed.cu:654-659).
+    msg = kvszp.last_error()
+    if msg:
+        print(f"Error: {where}: {msg}", file=sys.stderr)
+
+
+class CuSZpWrapper:
+    """CuSZpWrapper (cuszp_wrapper.h:9-158) on the MI355X HIP codec."""
+
+    def __init__(self, config: CompressionConfig, device_id: int = 0):
+        self._config = config._copy()
+        self._device_id = int(device_id)
+        self._ctx = kvszp.Context(self._config._to_c(), self._device_id)
+
+    # ---- configuration -------------------------------------------------
+
+    def get_config(self) -> CompressionConfig:
+        return self._config._copy()
+
+    def update_config(self, config: CompressionConfig) -> None:
+        self._config = config._copy()
+        self._ctx.update_config(self._config._to_c())
+
+    def set_codec_options(self, quantizer: int = kvszp.QUANT_TWO_ROUNDINGS,
+                          rate0_policy: int = kvszp.RATE0_ZERO) -> None:
+        """Codec switches with no reference counterpart: the quantizer
+        reading of the reference's PTX, and whether rate-0 blocks are written
+        as +0.0 or left untouched (the reference leaves them untouched)."""
+        self._ctx.set_options(quantizer, rate0_policy)
+
+    @staticmethod
+    def estimate_compressed_buffer_size(original_size: int) -> int:
+        return int(original_size) * 2  # cuszp_wrapper.cpp:1319-1321
+
+    # ---- helpers ---------------------------------------------------------
+
+    def _on_device(self, t: torch.Tensor) -> bool:
+        return t.is_cuda and t.get_device() == self._device_id
+
+    def _compress_inputs_ok(self, inputs, outputs, eps_overrides,
+                            min_numel: int, exact_numel: bool,
+                            capacity: int) -> bool:
+        for inp, out in zip(inputs, outputs):
+            if not (self._on_device(inp) and self._on_device(out)):
+                return False
+            if inp.dtype != torch.bfloat16 or out.dtype != torch.uint8:
+                return False
+            if not (inp.is_contiguous() and out.is_contiguous()):
+                return False
+            numel = inp.numel()
+            if (numel != min_numel) if exact_numel else (numel < min_numel):
+                return False
+            if out.numel() < capacity:
+                return False
+        return True
+
+    @staticmethod
+    def _eps_array(eps_overrides, batch: int):
+        if not eps_overrides:
+            return None
+        return kvszp.f32_array([_f32(e) for e in eps_overrides])
+
+    def _fixed_mode(self) -> bool:
+        c = self._config
+        return (c.processing_dim == CuszpDim.DIM_1D
+                and c.data_type == CuszpType.TYPE_FLOAT
+                and c.encoding_mode == CuszpMode.MODE_FIXED)
+
+    def _finish_compress(self, rc: int, batch: int, sizes, bounds, where: str):
+        if rc != kvszp.OK:
+            _report(where)
+            return (False, [], [])
+        return (True, [int(sizes[i]) for i in range(batch)],
+                [float(bounds[i]) for i in range(batch)])
+
+    # ---- batched BF16 compress -----------------------------------------
+
+    def compress_batch_fixed_bf16(self, input_tensors, compressed_buffers,
+                                  eps_overrides):
+        """pybind11_bindings.cpp:84-101 -> cuszp_wrapper.cpp:431-544."""
+        batch = len(input_tensors)
+        if (batch == 0 or len(compressed_buffers) != batch
+                or (eps_overrides and len(eps_overrides) != batch)
+                or not self._fixed_mode()):
+            return (False, [], [])
+        n = input_tensors[0].numel()
+        if not self._compress_inputs_ok(input_tensors, compressed_buffers,
+                                        eps_overrides, n, True,
+                                        self.estimate_compressed_buffer_size(4 * n)):
+            return (False, [], [])
+        sizes = (ctypes.c_uint64 * batch)()
+        bounds = (ctypes.c_float * batch)()
+        rc = self._ctx.compress(
+            kvszp.ptr_array([t.data_ptr() for t in input_tensors]),
+            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
+            kvszp.u64_array([t.numel() for t in compressed_buffers]),
+            self._eps_array(eps_overrides, batch), batch, n,
+            _stream_handle(self._device_id), sizes, bounds)
+        return self._finish_compress(rc, batch, sizes, bounds,
+                                     "fixed BF16 batch compression failed")
+
+    def _layer_index_ok(self, layer_indices: torch.Tensor,
+                        source_layers: int) -> bool:
+        sel = layer_indices.numel()
+        return (sel > 0 and sel <= source_layers and self._on_device(layer_indices)
+                and layer_indices.dtype == torch.int64
+                and layer_indices.is_contiguous())
+
+    def compress_batch_fixed_bf16_indexed(self, input_tensors,
+                                          compressed_buffers, layer_indices,
+                                          prefix_count, source_layers,
+                                          elements_per_layer, eps_overrides):
+        """pybind11_bindings.cpp:104-132 -> cuszp_wrapper.cpp:548-681."""
+        batch = len(input_tensors)
+        if (batch == 0 or len(compressed_buffers) != batch
+                or (eps_overrides and len(eps_overrides) != batch)
+                or prefix_count == 0 or source_layers == 0
+                or elements_per_layer == 0
+                or not self._layer_index_ok(layer_indices, source_layers)
+                or not self._fixed_mode()):
+            return (False, [], [])
+        sel = layer_indices.numel()
+        source_elements = prefix_count * source_layers * elements_per_layer
+        n = prefix_count * sel * elements_per_layer
+        if not self._compress_inputs_ok(input_tensors, compressed_buffers,
+                                        eps_overrides, source_elements, False,
+                                        self.estimate_compressed_buffer_size(4 * n)):
+            return (False, [], [])
+        sizes = (ctypes.c_uint64 * batch)()
+        bounds = (ctypes.c_float * batch)()
+        rc = self._ctx.compress_indexed(
+            kvszp.ptr_array([t.data_ptr() for t in input_tensors]),
+            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
+            kvszp.u64_array([t.numel() for t in compressed_buffers]),
+            layer_indices.data_ptr(), sel, prefix_count, source_layers,
+            elements_per_layer, self._eps_array(eps_overrides, batch), batch,
+            _stream_handle(self._device_id), sizes, bounds)
+        return self._finish_compress(rc, batch, sizes, bounds,
+                                     "indexed fixed BF16 batch compression failed")
+
+    def compress_batch_fixed_bf16_indexed_groups(self, input_tensors,
+                                                 compressed_buffers,
+                                                 layer_indices, group_sizes,
+                                                 prefix_count, source_layers,
+                                                 elements_per_layer,
+                                                 eps_overrides):
+        """pybind11_bindings.cpp:133-163 -> cuszp_wrapper.cpp:683-868."""
+        batch = len(input_tensors)
+        if (batch == 0 or len(compressed_buffers) != batch
+                or (eps_overrides and len(eps_overrides) != batch)
+                or not layer_indices or len(layer_indices) != len(group_sizes)
+                or prefix_count == 0 or source_layers == 0
+                or elements_per_layer == 0 or not self._fixed_mode()):
+            return (False, [], [])
+        for size, idx in zip(group_sizes, layer_indices):
+            if size == 0 or not self._layer_index_ok(idx, source_layers):
+                return (False, [], [])
+        if sum(group_sizes) != batch:
+            return (False, [], [])
+        source_elements = prefix_count * source_layers * elements_per_layer
+        offset = 0
+        for size, idx in zip(group_sizes, layer_indices):
+            n = prefix_count * idx.numel() * elements_per_layer
+            if not self._compress_inputs_ok(
+                    input_tensors[offset:offset + size],
+                    compressed_buffers[offset:offset + size], None,
+                    source_elements, False,
+                    self.estimate_compressed_buffer_size(4 * n)):
+                return (False, [], [])
+            offset += size
+        groups = len(group_sizes)
+        sizes = (ctypes.c_uint64 * batch)()
+        bounds = (ctypes.c_float * batch)()
+        rc = self._ctx.compress_indexed_groups(
+            kvszp.ptr_array([t.data_ptr() for t in input_tensors]),
+            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
+            kvszp.u64_array([t.numel() for t in compressed_buffers]),
+            kvszp.ptr_array([t.data_ptr() for t in layer_indices]),
+            kvszp.size_array([t.numel() for t in layer_indices]),
+            kvszp.size_array([int(s) for s in group_sizes]), groups,
+            prefix_count, source_layers, elements_per_layer,
+            self._eps_array(eps_overrides, batch), batch,
+            _stream_handle(self._device_id), sizes, bounds)
+        return self._finish_compress(
+            rc, batch, sizes, bounds,
+            "grouped indexed fixed BF16 batch compression failed")
+
+    # ---- batched BF16 decompress -----------------------------------------
+
+    def _streams_ok(self, compressed_buffers, compressed_sizes) -> bool:
+        return all(self._on_device(t) and int(s) != 0
+                   for t, s in zip(compressed_buffers, compressed_sizes))
+
+    def decompress_batch_fixed_bf16(self, compressed_buffers,
+                                    compressed_sizes, output_tensor,
+                                    num_elements_per_page,
+                                    actual_error_bounds):
+        """pybind11_bindings.cpp:190-207 -> cuszp_wrapper.cpp:1034-1110."""
+        batch = len(compressed_buffers)
+        if batch == 0:
+            return True
+        if (len(compressed_sizes) != batch or len(actual_error_bounds) != batch
+                or num_elements_per_page == 0 or not output_tensor.is_cuda
+                or output_tensor.dtype != torch.bfloat16
+                or output_tensor.numel() < batch * num_elements_per_page
+                or not self._fixed_mode()
+                or not self._streams_ok(compressed_buffers, compressed_sizes)):
+            print("Error: invalid cuSZp fixed BF16 batch metadata", file=sys.stderr)
+            return False
+        rc = self._ctx.decompress(
+            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
+            kvszp.u64_array([int(s) for s in compressed_sizes]),
+            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
+            output_tensor.data_ptr(), output_tensor.numel(),
+            num_elements_per_page, _stream_handle(self._device_id))
+        if rc != kvszp.OK:
+            _report("fixed BF16 batch decompression failed")
+            return False
+        return True
+
+    def decompress_batch_fixed_bf16_scatter(self, compressed_buffers,
+                                            compressed_sizes, output_tensors,
+                                            num_elements_per_page,
+                                            destinations_per_page,
+                                            elements_per_destination,
+                                            actual_error_bounds):
+        """pybind11_bindings.cpp:208-230 -> cuszp_wrapper.cpp:1111-1212."""
+        batch = len(compressed_buffers)
+        if batch == 0:
+            return True
+        if (len(compressed_sizes) != batch or len(actual_error_bounds) != batch
+                or destinations_per_page == 0 or elements_per_destination == 0
+                or num_elements_per_page
+                != destinations_per_page * elements_per_destination
+                or len(output_tensors) != batch * destinations_per_page
+                or not self._fixed_mode()
+                or not self._streams_ok(compressed_buffers, compressed_sizes)):
+            print("Error: invalid cuSZp direct-scatter metadata", file=sys.stderr)
+            return False
+        for out in output_tensors:
+            if (not out.is_cuda or out.dtype != torch.bfloat16
+                    or not out.is_contiguous()
+                    or out.numel() < elements_per_destination):
+                print("Error: invalid BF16 direct-scatter destination",
+                      file=sys.stderr)
+                return False
+        rc = self._ctx.decompress_scatter(
+            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
+            kvszp.u64_array([int(s) for s in compressed_sizes]),
+            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
+            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
+            num_elements_per_page, destinations_per_page,
+            elements_per_destination, _stream_handle(self._device_id))
+        if rc != kvszp.OK:
+            _report("fixed BF16 direct-scatter decompression failed")
+            return False
+        return True
+
+    def decompress_batch_fixed_bf16_indexed_scatter(self, compressed_buffers,
+                                                    compressed_sizes,
+                                                    output_tensors,
+                                                    layer_indices,
+                                                    prefix_count,
+                                                    source_layers,
+                                                    elements_per_layer,
+                                                    actual_error_bounds):
+        """pybind11_bindings.cpp:232-256 -> cuszp_wrapper.cpp:1214-1313."""
+        batch = len(compressed_buffers)
+        if batch == 0:
+            return True
+        if (len(compressed_sizes) != batch or len(actual_error_bounds) != batch
+                or len(output_tensors) != batch or prefix_count == 0
+                or source_layers == 0 or elements_per_layer == 0
+                or not self._layer_index_ok(layer_indices, source_layers)
+                or not self._fixed_mode()):
+            return False
+        source_elements = prefix_count * source_layers * elements_per_layer
+        for comp, size, out in zip(compressed_buffers, compressed_sizes,
+                                   output_tensors):
+            if (not self._on_device(comp) or int(size) == 0
+                    or not self._on_device(out)
+                    or out.dtype != torch.bfloat16 or not out.is_contiguous()
+                    or out.numel() < source_elements):
+                return False
+        rc = self._ctx.decompress_indexed_scatter(
+            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
+            kvszp.u64_array([int(s) for s in compressed_sizes]),
+            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
+            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
+            layer_indices.data_ptr(), layer_indices.numel(), prefix_count,
+            source_layers, elements_per_layer, _stream_handle(self._device_id))
+        if rc != kvszp.OK:
+            _report("indexed fixed BF16 scatter decompression failed")
+            return False
+        return True
+
+    def synchronize(self) -> bool:
+        """Waits for the current stream and reports device-side errors of
+        earlier (enqueue-only) decompress calls.  No reference counterpart."""
+        rc = self._ctx.synchronize(_stream_handle(self._device_id))
+        if rc != kvszp.OK:
+            _report("device-side codec error")
+            return False
+        return True
+
+    # ---- single-page fp32 API (upstream cuSZp kernels; not implemented) ---
+
+    def compress(self, input_tensor, compressed_buffer, eps_override=-1.0):
+        """pybind11_bindings.cpp:49-64 (upstream fp32 codec)."""
+        print("Error: fp32 single-page cuSZp compress is not provided by this "
+              "codec", file=sys.stderr)
+        return (False, compressed_buffer, 0, 0.0)
+
+    def compress_batch_fixed(self, input_tensors, compressed_buffers,
+                             eps_overrides):
+        """pybind11_bindings.cpp:65-82 (upstream fp32 codec)."""
+        return (False, [], [])
+
+    def decompress(self, compressed_buffer, compressed_size, output_tensor,
+                   actual_error_bound):
+        """pybind11_bindings.cpp:164-173 (upstream fp32 codec)."""
+        print("Error: fp32 single-page cuSZp decompress is not provided by "
+              "this codec", file=sys.stderr)
+        return False
+
+    def decompress_batch(self, compressed_buffers, compressed_sizes,
+                         output_tensors, actual_error_bounds):
+        """pybind11_bindings.cpp:174-189 (upstream fp32 codec)."""
+        return False
