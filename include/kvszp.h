@@ -163,6 +163,18 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter(
  * counterpart: the reference's decoders have no device-side checks. */
 int kvszp_synchronize(kvszp_ctx* ctx, kvszp_stream_t stream);
 
+/* Kernel timing.  When enabled, every launch of this context is bracketed
+ * by HIP events recorded on the launch stream (compress: relative-bound
+ * pre-pass, if any, plus encoder; decompress: decoder).  kvszp_drain_timing
+ * waits for the recorded events, returns the summed milliseconds and launch
+ * counts per kind, and forgets them.  No reference counterpart: the
+ * reference times whole stages with synchronize + perf_counter
+ * (vllm_v1_compressed_offload.py:2009-2019). */
+enum { KVSZP_KERNEL_COMPRESS = 0, KVSZP_KERNEL_DECOMPRESS = 1 };
+int kvszp_enable_timing(kvszp_ctx* ctx, int enable);
+int kvszp_drain_timing(kvszp_ctx* ctx, double* compress_ms, int* compress_count,
+                       double* decompress_ms, int* decompress_count);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* kvszp_last_error(void);
 

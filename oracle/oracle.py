@@ -15,6 +15,7 @@ from __future__ import annotations
 import ctypes
 import os
 import subprocess
+import time
 
 import numpy as np
 
@@ -226,9 +227,11 @@ def decompress_indexed(stream, n: int, eb: float, destination: np.ndarray,
 def compress_batch(pages: np.ndarray, eps, default_eps: float = 1e-4,
                    relative: bool = True, variant: int = QUANT_TWO_ROUNDINGS,
                    threads: int = 1, layer_indices=None, source_layers: int = 0,
-                   elements_per_layer: int = 0, n: int | None = None):
+                   elements_per_layer: int = 0, n: int | None = None,
+                   return_elapsed: bool = False):
     """Encode ``pages`` (shape [B, page_numel], uint16) like the reference's
-    batched call.  Returns (list of stream arrays, sizes, bounds)."""
+    batched call.  Returns (list of stream arrays, sizes, bounds), plus the
+    seconds spent in the C encoder when ``return_elapsed``."""
     pages = _as_u16(pages)
     batch = pages.shape[0]
     idx, p = _layer_args(layer_indices)
@@ -246,11 +249,15 @@ def compress_batch(pages: np.ndarray, eps, default_eps: float = 1e-4,
         np.asarray(eps, dtype=np.float32))
     sizes = np.zeros(batch, dtype=np.uint64)
     bounds = np.zeros(batch, dtype=np.float32)
+    t0 = time.perf_counter()
     lib().kvo_compress_batch(page_ptrs, out_ptrs, batch, n, p, sel,
                              source_layers, elements_per_layer, _ptr(eps_arr),
                              default_eps, int(relative), variant, threads,
                              sizes.ctypes.data, bounds.ctypes.data)
+    elapsed = time.perf_counter() - t0
     streams = [outs[i, :int(sizes[i])].copy() for i in range(batch)]
+    if return_elapsed:
+        return streams, sizes, bounds, elapsed
     return streams, sizes, bounds
 
 

@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -58,6 +59,12 @@ constexpr uint32_t kEpochLimit = (1u << 30) - 2u;
 constexpr uint64_t kMaxElements = 1ull << 29;      // per logical segment
 constexpr uint64_t kMaxTiles = (1ull << 32) / kThreads - 1;
 
+struct TimingRecord {
+    int kind;  // KVSZP_KERNEL_*
+    hipEvent_t start, stop;
+    double bytes;  // algorithmic bytes of the launch (filled when known)
+};
+
 struct GroupSpec {
     uint64_t n;
     const int64_t* layers;
@@ -73,6 +80,7 @@ struct kvszp_ctx {
     int quantizer = KVSZP_QUANT_TWO_ROUNDINGS;
     int rate0 = KVSZP_RATE0_ZERO;
     uint32_t fused_tile_limit = 0;
+    bool use_tickets = false;  // KVSZP_TICKETS=1: ticket-ordered tiles
     // control words: [0] ticket counter, [1] low 32 bits = error word
     unsigned long long* control = nullptr;
     unsigned long long ticket_next = 0;
@@ -82,6 +90,10 @@ struct kvszp_ctx {
     int next_slot = 0;
     void* host_results = nullptr;
     size_t host_results_bytes = 0;
+    // Optional kernel timing: event pairs recorded on the launch stream.
+    bool timing = false;
+    std::vector<TimingRecord> timed;      // recorded, not yet drained
+    std::vector<hipEvent_t> spare_events;
 };
 
 namespace {
@@ -195,6 +207,36 @@ int check_fixed_config(const kvszp_ctx* c) {
         return fail(KVSZP_EINVAL,
                     "batched BF16 codec requires MODE_FIXED, DIM_1D, TYPE_FLOAT");
     return KVSZP_OK;
+}
+
+hipEvent_t take_event(kvszp_ctx* c) {
+    if (!c->spare_events.empty()) {
+        hipEvent_t e = c->spare_events.back();
+        c->spare_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Starts a timed region on `stream` when timing is enabled; returns the index
+// of the record or -1.
+int timing_begin(kvszp_ctx* c, int kind, hipStream_t stream) {
+    if (!c->timing) return -1;
+    TimingRecord r{kind, take_event(c), take_event(c), 0.0};
+    if (!r.start || !r.stop || hipEventRecord(r.start, stream) != hipSuccess) {
+        if (r.start) c->spare_events.push_back(r.start);
+        if (r.stop) c->spare_events.push_back(r.stop);
+        return -1;
+    }
+    c->timed.push_back(r);
+    return (int)c->timed.size() - 1;
+}
+
+void timing_end(kvszp_ctx* c, int rec, hipStream_t stream) {
+    if (rec < 0) return;
+    (void)hipEventRecord(c->timed[rec].stop, stream);
 }
 
 uint32_t header_bytes_of(uint64_t n) {
@@ -326,6 +368,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     const CompressJob* djobs = reinterpret_cast<const CompressJob*>(c->tables.ptr);
 
     hipError_t e;
+    const int rec = timing_begin(c, KVSZP_KERNEL_COMPRESS, stream);
     if (bound_mode == kBoundPrepass) {
         MinMaxParams m;
         std::memset(&m, 0, sizeof(m));
@@ -345,7 +388,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     p.job_size = job_size;
     p.job_eb = job_eb;
     p.error = error_word(c);
-    p.ticket = c->control;
+    p.ticket = c->use_tickets ? c->control : nullptr;
     p.ticket_base = c->ticket_next;
     p.epoch = epoch;
     p.total_tiles = (uint32_t)total_tiles;
@@ -355,6 +398,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     p.aligned16 = aligned16 ? 1 : 0;
     e = launch_compress(p, stream);
     if (e != hipSuccess) return hip_fail(e, "compress launch");
+    timing_end(c, rec, stream);
     c->ticket_next += total_tiles;
 
     // One D2H of sizes (+ bounds) and the error word, then wait: callers need
@@ -437,7 +481,7 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         reinterpret_cast<char*>(c->tables.ptr) + jobs_bytes);
     p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
     p.error = error_word(c);
-    p.ticket = c->control;
+    p.ticket = c->use_tickets ? c->control : nullptr;
     p.ticket_base = c->ticket_next;
     p.epoch = epoch;
     p.total_tiles = (uint32_t)total_tiles;
@@ -457,8 +501,10 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     g.first_tile = 0;
     g.tiles_per_job = tiles_per_job;
     g.header_bytes = R;
+    const int rec = timing_begin(c, KVSZP_KERNEL_DECOMPRESS, stream);
     hipError_t e = launch_decompress(p, stream);
     if (e != hipSuccess) return hip_fail(e, "decompress launch");
+    timing_end(c, rec, stream);
     c->ticket_next += total_tiles;
     return KVSZP_OK;
 }
@@ -488,6 +534,10 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
         c->config.data_type = KVSZP_TYPE_FLOAT;
     }
     c->device = device_id;
+    {
+        const char* env = std::getenv("KVSZP_TICKETS");
+        c->use_tickets = env && env[0] == '1';
+    }
     e = hipMalloc(&c->control, 64);
     if (e == hipSuccess) e = hipMemset(c->control, 0, 64);
     for (int i = 0; e == hipSuccess && i < kSlots; ++i)
@@ -515,6 +565,11 @@ int kvszp_destroy(kvszp_ctx* c) {
         }
         if (s.host) (void)hipHostFree(s.host);
     }
+    for (auto& r : c->timed) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    for (hipEvent_t ev : c->spare_events) (void)hipEventDestroy(ev);
     DevBuf* bufs[5] = {&c->tile_state, &c->tile_minmax, &c->job_minmax,
                        &c->tables, &c->results};
     for (DevBuf* b : bufs)
@@ -725,6 +780,39 @@ int kvszp_synchronize(kvszp_ctx* c, kvszp_stream_t stream) {
         return rc;
     }
     return KVSZP_OK;
+}
+
+int kvszp_enable_timing(kvszp_ctx* c, int enable) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    c->timing = enable != 0;
+    return KVSZP_OK;
+}
+
+int kvszp_drain_timing(kvszp_ctx* c, double* compress_ms, int* compress_count,
+                       double* decompress_ms, int* decompress_count) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    double ms[2] = {0.0, 0.0};
+    int count[2] = {0, 0};
+    int rc = KVSZP_OK;
+    for (auto& r : c->timed) {
+        float t = 0.0f;
+        hipError_t e = hipEventSynchronize(r.stop);
+        if (e == hipSuccess) e = hipEventElapsedTime(&t, r.start, r.stop);
+        if (e != hipSuccess) {
+            rc = hip_fail(e, "timing events");
+        } else if (r.kind == KVSZP_KERNEL_COMPRESS || r.kind == KVSZP_KERNEL_DECOMPRESS) {
+            ms[r.kind] += t;
+            count[r.kind] += 1;
+        }
+        c->spare_events.push_back(r.start);
+        c->spare_events.push_back(r.stop);
+    }
+    c->timed.clear();
+    if (compress_ms) *compress_ms = ms[KVSZP_KERNEL_COMPRESS];
+    if (compress_count) *compress_count = count[KVSZP_KERNEL_COMPRESS];
+    if (decompress_ms) *decompress_ms = ms[KVSZP_KERNEL_DECOMPRESS];
+    if (decompress_count) *decompress_count = count[KVSZP_KERNEL_DECOMPRESS];
+    return rc;
 }
 
 const char* kvszp_last_error(void) { return g_last_error.c_str(); }

@@ -60,8 +60,14 @@ __device__ __forceinline__ void flag_error(uint32_t* e, uint32_t bits) {
     __hip_atomic_fetch_or(e, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Tile number of this workgroup.  With a ticket counter the number is the
+// order in which workgroups started, so every tile a workgroup waits for has
+// already started.  Without one it is blockIdx.x, which relies on the
+// dispatcher starting workgroups in index order (one atomic per tile on a
+// single address serializes at the memory side, so this is the fast mode).
 __device__ __forceinline__ uint32_t take_ticket(unsigned long long* ticket,
                                                 unsigned long long base) {
+    if (ticket == nullptr) return blockIdx.x;
     return (uint32_t)(__hip_atomic_fetch_add(ticket, 1ull, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT) -
                       base);

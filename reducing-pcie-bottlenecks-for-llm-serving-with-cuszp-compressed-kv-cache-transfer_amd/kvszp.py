@@ -57,6 +57,8 @@ EXPORTS = [
     ("kvszp_decompress_batch_fixed_bf16_indexed_scatter", _i,
      [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
     ("kvszp_synchronize", _i, [_vp, _vp]),
+    ("kvszp_enable_timing", _i, [_vp, _i]),
+    ("kvszp_drain_timing", _i, [_vp, _vp, _vp, _vp, _vp]),
     ("kvszp_last_error", ctypes.c_char_p, []),
 ]
 
@@ -83,9 +85,19 @@ _lib: ctypes.CDLL | None = None
 
 
 def load() -> ctypes.CDLL:
-    """Loads libkvszp.so; raises if it has not been built."""
+    """Loads libkvszp.so; raises if it has not been built.
+
+    PyTorch-ROCm bundles its own HIP runtime under the same SONAME
+    (libamdhip64.so.7) as the system ROCm one libkvszp.so is linked against.
+    Whichever is loaded first serves the process; loading both breaks device
+    discovery.  So when torch is installed it is imported first and the
+    codec runs on torch's runtime, sharing its streams."""
     global _lib
     if _lib is None:
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise ImportError(
                 f"{LIB_PATH} is missing: build it with build.py (hipcc, gfx950)")
@@ -214,6 +226,20 @@ class Context:
 
     def synchronize(self, stream) -> int:
         return self._lib.kvszp_synchronize(self.handle, stream)
+
+    def enable_timing(self, enable: bool = True) -> None:
+        check(self._lib.kvszp_enable_timing(self.handle, int(enable)))
+
+    def drain_timing(self) -> dict:
+        """Summed kernel milliseconds and launch counts since the last drain,
+        from HIP events recorded on the launch stream."""
+        cms, dms = ctypes.c_double(), ctypes.c_double()
+        cc, dc = ctypes.c_int(), ctypes.c_int()
+        check(self._lib.kvszp_drain_timing(
+            self.handle, ctypes.byref(cms), ctypes.byref(cc), ctypes.byref(dms),
+            ctypes.byref(dc)))
+        return {"compress_ms": cms.value, "compress_launches": cc.value,
+                "decompress_ms": dms.value, "decompress_launches": dc.value}
 
 
 def header_bytes(n: int) -> int:
