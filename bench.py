@@ -206,6 +206,9 @@ def main() -> int:
     ap.add_argument("--cpu-pages", type=int, default=256,
                     help="pages of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy (the reference "
+                         "kernel for scaling rocprof FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -216,6 +219,15 @@ def main() -> int:
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_calibration:
+        src = torch.ones(128 << 20, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 2,
+                          "copies": 3}), flush=True)
+        return 0
     log("building workload")
     w = Workload(args.seed)
     log(f"workload: {w.num_pages} pages x {w.page_numel} BF16, "

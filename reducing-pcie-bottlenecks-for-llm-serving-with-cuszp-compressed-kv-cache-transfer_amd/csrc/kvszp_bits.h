@@ -2,21 +2,25 @@
 // stream, shared by the encoder and decoder kernels.  Pure functions on
 // uint32_t arrays so the host test suite can check them with g++.
 //
-// Stream word layout (reference: cuszp_batched_fixed.cu:320-351): in the
-// sign word and in plane word p of a 32-element block, element v sits in
-// byte v>>3 at bit 7-(v&7), i.e. at bit (v ^ 7) of the little-endian u32.
+// Stream word layout (reference: cuszp_batched_fixed.cu:320-351): a block
+// with rate r > 0 is stored as words w_0 .. w_r, where w_0 is the sign word
+// and w_{1+p} is bit plane p of |q|.  In every word, element v of the block
+// sits in byte v>>3 at bit 7-(v&7), i.e. at bit (v ^ 7) of the
+// little-endian u32.
 //
-// Both directions are the same bit-matrix transpose, because a transpose is
-// its own inverse:
-//   rows-by-element  A[k] = a[k^7]      (a = |q| with the sign in the top bit)
-//   rows-by-plane    A[b] = word b      (plane words, sign word last)
-// Two widths are provided:
-//   * 16-bit fields (rates <= 15): two independent 16x16 matrices share the
-//     dword halves.  A[k] = f[k^7] | f[16+(k^7)] << 16 with
-//     f = |q| | sign << 15; after the transpose A[b] is plane word b for
-//     b < 15 and A[15] is the sign word.  4 stages on 16 dwords.
-//   * 32-bit fields (any rate): A[k] = a[k^7] with a = |q| | sign << 31;
-//     after the transpose A[b] is plane b (b <= 30) and A[31] the sign word.
+// Register layout.  Each element is turned into a 16-bit FIELD and two
+// fields share a dword: row k holds element k^7 in the low half and element
+// 16+(k^7) in the high half.  A 16x16 bit-matrix transpose of each half
+// (transpose16x2) turns "row k = field of one element" into "row b = bit b
+// of every field, one bit per element at position v^7" -- i.e. row b IS a
+// stream word.  With the field
+//     f_lo = ((|q| << 1) | sign) & 0xFFFF
+// row 0 is the sign word and row 1+p is plane p, so rows 0..15 are stream
+// words w_0..w_15: a block with rate <= 15 is finished in one transpose.  For
+// rates 16..31 a second pass with
+//     f_hi = (|q| >> 15) & 0xFFFF
+// yields planes 15..30 = words w_16..w_31.  The transpose is its own
+// inverse, which is how the decoder gets the fields back.
 #ifndef KVSZP_BITS_H
 #define KVSZP_BITS_H
 
@@ -30,9 +34,9 @@
 
 namespace kvszp {
 
-// Exchange the columns {c : c & j} of x with the columns {c : !(c & j)} of y
+// Exchange the columns {c : c & J} of x with the columns {c : !(c & J)} of y
 // (the block-swap step of a recursive bit-matrix transpose).  `mask` selects
-// the columns with (c & j) == 0.
+// the columns with (c & J) == 0.
 template <int J>
 KVSZP_HD void delta_swap(uint32_t& x, uint32_t& y, uint32_t mask) {
     const uint32_t t = ((x >> J) ^ y) & mask;
@@ -56,53 +60,47 @@ KVSZP_HD void transpose16x2(uint32_t* a) {
         if ((k & 1) == 0) delta_swap<1>(a[k], a[k + 1], 0x55555555u);
 }
 
-// Transposes a 32x32 bit matrix held in rows [0,32).
-KVSZP_HD void transpose32(uint32_t* a) {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) delta_swap<16>(a[k], a[k + 16], 0x0000FFFFu);
-#pragma unroll
-    for (int k = 0; k < 32; ++k)
-        if ((k & 8) == 0) delta_swap<8>(a[k], a[k + 8], 0x00FF00FFu);
-#pragma unroll
-    for (int k = 0; k < 32; ++k)
-        if ((k & 4) == 0) delta_swap<4>(a[k], a[k + 4], 0x0F0F0F0Fu);
-#pragma unroll
-    for (int k = 0; k < 32; ++k)
-        if ((k & 2) == 0) delta_swap<2>(a[k], a[k + 2], 0x33333333u);
-#pragma unroll
-    for (int k = 0; k < 32; ++k)
-        if ((k & 1) == 0) delta_swap<1>(a[k], a[k + 1], 0x55555555u);
-}
+// Element held in the low / high half of row k.
+KVSZP_HD int row_lo_elem(int k) { return k ^ 7; }
+KVSZP_HD int row_hi_elem(int k) { return 16 + (k ^ 7); }
 
-// Magnitude-with-sign a = |q| | sign<<31 -> 16-bit field |q| | sign<<15.
-// Valid when |q| < 2^15.
-KVSZP_HD uint32_t field16(uint32_t a) {
-    return (a & 0x7FFFu) | ((a >> 16) & 0x8000u);
-}
+// 16-bit fields of a magnitude m = |q| (< 2^31) and sign s (0/1).
+KVSZP_HD uint32_t field_lo(uint32_t m, uint32_t s) { return ((m << 1) | s) & 0xFFFFu; }
+KVSZP_HD uint32_t field_hi(uint32_t m) { return (m >> 15) & 0xFFFFu; }
 
-// Encoder: a[32] (|q| | sign<<31, element order) -> words[0] = sign word,
-// words[1 + p] = plane p.
-// Narrow form: every |q| < 2^15, 16 words out (planes 0..14).
-KVSZP_HD void pack_block_words_narrow(const uint32_t* a, uint32_t* words) {
+// Reference-free host helpers (used by the host test): a[v] = |q_v| with the
+// sign in bit 31, element order.  words[0..31] receive w_0..w_31.
+KVSZP_HD void pack_block_words(const uint32_t* a, uint32_t* words) {
     uint32_t m[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k)
-        m[k] = field16(a[k ^ 7]) | (field16(a[16 + (k ^ 7)]) << 16);
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t lo = a[row_lo_elem(k)], hi = a[row_hi_elem(k)];
+        m[k] = field_lo(lo & 0x7FFFFFFFu, lo >> 31) |
+               (field_lo(hi & 0x7FFFFFFFu, hi >> 31) << 16);
+    }
     transpose16x2(m);
-    words[0] = m[15];
-#pragma unroll
-    for (int p = 0; p < 15; ++p) words[1 + p] = m[p];
+    for (int b = 0; b < 16; ++b) words[b] = m[b];
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t lo = a[row_lo_elem(k)], hi = a[row_hi_elem(k)];
+        m[k] = field_hi(lo & 0x7FFFFFFFu) | (field_hi(hi & 0x7FFFFFFFu) << 16);
+    }
+    transpose16x2(m);
+    for (int b = 0; b < 16; ++b) words[16 + b] = m[b];
 }
 
-// Wide form: any |q| < 2^31, 32 words out (planes 0..30).
-KVSZP_HD void pack_block_words_wide(const uint32_t* a, uint32_t* words) {
-    uint32_t m[32];
-#pragma unroll
-    for (int k = 0; k < 32; ++k) m[k] = a[k ^ 7];
-    transpose32(m);
-    words[0] = m[31];
-#pragma unroll
-    for (int p = 0; p < 31; ++p) words[1 + p] = m[p];
+KVSZP_HD void unpack_block_words(const uint32_t* words, uint32_t* a) {
+    uint32_t lo[16], hi[16];
+    for (int b = 0; b < 16; ++b) {
+        lo[b] = words[b];
+        hi[b] = words[16 + b];
+    }
+    transpose16x2(lo);
+    transpose16x2(hi);
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t fl0 = lo[k] & 0xFFFFu, fl1 = lo[k] >> 16;
+        const uint32_t fh0 = hi[k] & 0xFFFFu, fh1 = hi[k] >> 16;
+        a[row_lo_elem(k)] = ((fl0 >> 1) | (fh0 << 15)) | ((fl0 & 1u) << 31);
+        a[row_hi_elem(k)] = ((fl1 >> 1) | (fh1 << 15)) | ((fl1 & 1u) << 31);
+    }
 }
 
 }  // namespace kvszp

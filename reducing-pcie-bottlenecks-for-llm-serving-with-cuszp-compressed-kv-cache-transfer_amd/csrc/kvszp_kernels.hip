@@ -44,6 +44,17 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* to_global(T* p) 
     return (__attribute__((address_space(1))) T*)p;
 }
 
+// Read-only views of the per-call tables (job entries): the constant
+// address space lets a wave-uniform entry come through the scalar cache.
+template <typename T>
+__device__ __forceinline__ T load_const(const T* table, uint32_t i) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return ((const __attribute__((address_space(4))) T*)table)[i];
+#else
+    return table[i];  // host pass only parses this
+#endif
+}
+
 // ---- cross-workgroup primitives -------------------------------------------
 
 __device__ __forceinline__ unsigned long long load_relaxed(
@@ -234,7 +245,7 @@ __device__ __forceinline__ void load_block(
         const g_u32x4* p = (const g_u32x4*)to_global(in + src);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const u32x4 v = __builtin_nontemporal_load(p + i);
+            const u32x4 v = p[i];
             d[4 * i + 0] = v.x;
             d[4 * i + 1] = v.y;
             d[4 * i + 2] = v.z;
@@ -252,6 +263,61 @@ __device__ __forceinline__ void load_block(
         const uint32_t h = to_global(in)[s];
         d[v >> 1] |= (v & 1) ? (h << 16) : h;
     }
+}
+
+// Wave-cooperative load of the wave's 64 blocks when they are consecutive
+// in memory (wave_src = source of the wave's first block, 16-byte aligned):
+// four coalesced 1 KiB loads straight into LDS, then every lane reads its
+// own 64-byte block.  In load i, lane l fetches 16-byte chunk
+// 64i + 4(l%16) + l/16 of the wave's 4 KiB; global_load_lds puts lane l's
+// chunk at LDS slot 64i + l, so chunk c of block b sits at slot
+// 64(b/16) + (b%16) + 16c and the per-lane reads are bank-conflict free.
+__device__ __forceinline__ void wave_load_blocks(const uint16_t* wave_src,
+                                                 uint32_t* lds_wave, uint32_t* d) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t chunk = 4u * (lane & 15) + (lane >> 4);
+    const char* src = reinterpret_cast<const char*>(wave_src) + 16u * chunk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(src + 1024 * i),
+            (__attribute__((address_space(3))) void*)(lds_wave + 256 * i), 16, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): the LDS writes have landed
+    const u32x4* slots = reinterpret_cast<const u32x4*>(lds_wave);
+    const uint32_t base = 64u * (lane >> 4) + (lane & 15);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u32x4 v = slots[base + 16u * c];
+        d[4 * c + 0] = v.x;
+        d[4 * c + 1] = v.y;
+        d[4 * c + 2] = v.z;
+        d[4 * c + 3] = v.w;
+    }
+}
+
+// Loads this thread's block; whole waves whose 64 blocks are consecutive,
+// full and 16-byte aligned take the coalesced LDS path.
+__device__ __forceinline__ void load_block_wave(
+    const Group& g, const uint16_t* in, uint64_t tile_first_elem,
+    uint32_t elem_in_tile, uint32_t count, bool aligned16, uint32_t* d,
+    uint32_t* bad, uint32_t* lds_wave) {
+    uint64_t src = tile_first_elem + elem_in_tile;
+    bool contiguous = true;
+    if (g.layers != nullptr) {
+        const LayerCursor c = layer_cursor(g, tile_first_elem, elem_in_tile, bad);
+        src = c.src_index;
+        contiguous = c.contiguous;
+    }
+    const int lane = threadIdx.x & 63;
+    const uint64_t src0 = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(src >> 32)) << 32) |
+                          __builtin_amdgcn_readfirstlane((uint32_t)src);
+    const bool fast = count == kBlockElems && contiguous && aligned16 &&
+                      src == src0 + (uint64_t)kBlockElems * lane;
+    if (__ballot(!fast) == 0ull) {
+        wave_load_blocks(in + src0, lds_wave, d);
+        return;
+    }
+    load_block(g, in, tile_first_elem, elem_in_tile, count, aligned16, d, bad);
 }
 
 // ---- workgroup scan + decoupled look-back ---------------------------------
@@ -336,12 +402,26 @@ __device__ uint32_t lookback(unsigned long long* state, uint32_t t,
 }
 
 // Finds the group of tile t (groups are few and ordered by first_tile).
+// Unrolled over the kernel-argument table so the lookups are independent
+// scalar loads rather than a dependent chain.
 __device__ __forceinline__ int find_group(const Group* groups, int num_groups,
                                           uint32_t t) {
     int g = 0;
-    for (int i = 1; i < num_groups; ++i)
-        if (t >= groups[i].first_tile) g = i;
+#pragma unroll
+    for (int i = 1; i < kMaxGroups; ++i)
+        if (i < num_groups && t >= groups[i].first_tile) g = i;
     return g;
+}
+
+// Wave-uniform tile number.  Ticket mode broadcasts thread 0's ticket through
+// LDS (one barrier); otherwise the tile is blockIdx.x with no barrier.
+__device__ __forceinline__ uint32_t tile_number(unsigned long long* ticket,
+                                                unsigned long long base,
+                                                uint32_t* s_tile) {
+    if (ticket == nullptr) return blockIdx.x;
+    if (threadIdx.x == 0) *s_tile = take_ticket(ticket, base);
+    __syncthreads();
+    return __builtin_amdgcn_readfirstlane(*s_tile);
 }
 
 // ---- stream word I/O --------------------------------------------------------
@@ -349,6 +429,9 @@ __device__ __forceinline__ int find_group(const Group* groups, int num_groups,
 // them as 16-byte groups (unaligned 128-bit accesses) plus single words for
 // the tail; `cmax` is the wave-uniform maximum count, so groups no lane needs
 // are skipped without divergence.  Nothing outside [0, count) is touched.
+// Plain (cached) accesses on purpose: the L2 merges the lanes' partial
+// writes of a tile's contiguous payload into full lines, while non-temporal
+// stores reach HBM as partial-line writes (measured: ~4x the stream bytes).
 template <int kWords>
 __device__ __forceinline__ void store_words(uint32_t* dst, const uint32_t* w,
                                             uint32_t count, uint32_t cmax) {
@@ -362,12 +445,12 @@ __device__ __forceinline__ void store_words(uint32_t* dst, const uint32_t* w,
                 v.y = w[4 * j + 1];
                 v.z = w[4 * j + 2];
                 v.w = w[4 * j + 3];
-                __builtin_nontemporal_store(v, (g_u32x4_a4*)(d + 4 * j));
+                *(g_u32x4_a4*)(d + 4 * j) = v;
             } else {
 #pragma unroll
                 for (int i = 0; i < 3; ++i)
                     if (count > (uint32_t)(4 * j + i))
-                        __builtin_nontemporal_store(w[4 * j + i], d + 4 * j + i);
+                        d[4 * j + i] = w[4 * j + i];
             }
         }
     }
@@ -382,7 +465,7 @@ __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t* w,
         w[4 * j + 0] = w[4 * j + 1] = w[4 * j + 2] = w[4 * j + 3] = 0;
         if ((uint32_t)(4 * j) < cmax) {
             if (count >= (uint32_t)(4 * j + 4)) {
-                const u32x4 v = __builtin_nontemporal_load((const g_u32x4_a4*)(s + 4 * j));
+                const u32x4 v = *(const g_u32x4_a4*)(s + 4 * j);
                 w[4 * j + 0] = v.x;
                 w[4 * j + 1] = v.y;
                 w[4 * j + 2] = v.z;
@@ -391,9 +474,51 @@ __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t* w,
 #pragma unroll
                 for (int i = 0; i < 3; ++i)
                     if (count > (uint32_t)(4 * j + i))
-                        w[4 * j + i] = __builtin_nontemporal_load(s + 4 * j + i);
+                        w[4 * j + i] = s[4 * j + i];
             }
         }
+    }
+}
+
+// Quantized element v of a block held as 16 packed BF16 pairs; elements at
+// or past `count` quantize to 0 (cu:200-211).
+template <int kQuant, bool kFull>
+__device__ __forceinline__ int32_t quant_elem(const uint32_t* d, int v,
+                                              uint32_t count, float recip) {
+    const float x = (v & 1) ? bf16_hi(d[v >> 1]) : bf16_lo(d[v >> 1]);
+    const int32_t q = quantize<kQuant>(x, recip);
+    return (kFull || (uint32_t)v < count) ? q : 0;
+}
+
+__device__ __forceinline__ uint32_t magnitude(int32_t q) {
+    return (uint32_t)(q < 0 ? -q : q);  // q > INT_MIN always (cu:212-215)
+}
+
+// Rows of low fields ((|q| << 1) | sign) and the OR of all |q| (the rate is
+// its bit length, cu:221-222).
+template <int kQuant, bool kFull>
+__device__ __forceinline__ void build_rows_lo(const uint32_t* d, uint32_t count,
+                                              float recip, uint32_t* P,
+                                              uint32_t& orv) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int32_t q0 = quant_elem<kQuant, kFull>(d, row_lo_elem(k), count, recip);
+        const int32_t q1 = quant_elem<kQuant, kFull>(d, row_hi_elem(k), count, recip);
+        const uint32_t m0 = magnitude(q0), m1 = magnitude(q1);
+        orv |= m0 | m1;
+        P[k] = field_lo(m0, (uint32_t)q0 >> 31) | (field_lo(m1, (uint32_t)q1 >> 31) << 16);
+    }
+}
+
+// Rows of high fields (|q| >> 15), for rates above 15.
+template <int kQuant, bool kFull>
+__device__ __forceinline__ void build_rows_hi(const uint32_t* d, uint32_t count,
+                                              float recip, uint32_t* P) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t m0 = magnitude(quant_elem<kQuant, kFull>(d, row_lo_elem(k), count, recip));
+        const uint32_t m1 = magnitude(quant_elem<kQuant, kFull>(d, row_hi_elem(k), count, recip));
+        P[k] = field_hi(m0) | (field_hi(m1) << 16);
     }
 }
 
@@ -407,13 +532,12 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     __shared__ uint32_t s_max[kThreads / 64];
     __shared__ uint32_t s_prefix;
     __shared__ uint8_t s_rate[kTileBlocks];
+    __shared__ __attribute__((aligned(16))) uint32_t s_stage[kThreads / 64][1024];  // 4 KiB per wave
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    if (tid == 0) s_tile = take_ticket(p.ticket, p.ticket_base);
-    __syncthreads();
-    const uint32_t t = s_tile;
+    const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {  // tickets of another launch: never index past
         if (tid == 0) flag_error(p.error, kErrSpin);
         return;
@@ -421,10 +545,10 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
 
     const uint32_t local = t - g.first_tile;
-    const uint32_t job_in_group = local / g.tiles_per_job;
+    const uint32_t job_in_group = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
     const uint32_t tile = local - job_in_group * g.tiles_per_job;
     const uint32_t job = g.first_job + job_in_group;
-    const CompressJob J = p.jobs[job];
+    const CompressJob J = load_const(p.jobs, job);
     const uint64_t n = g.n;
     const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
     const uint32_t b = tile * kTileBlocks + tid;
@@ -435,8 +559,8 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
 
     uint32_t bad = 0;
     uint32_t d[16];
-    load_block(g, J.in, tile_first, (uint32_t)tid * kBlockElems, count,
-               p.aligned16 != 0, d, &bad);
+    load_block_wave(g, J.in, tile_first, (uint32_t)tid * kBlockElems, count,
+                    p.aligned16 != 0, d, &bad, &s_stage[wave][0]);
 
     float eb = J.eps;
     if (p.bound_mode != kBoundAbsolute) {
@@ -512,29 +636,14 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     }
     const float recip = 0.5f / eb;  // cu:166, IEEE division
 
-    // Quantize (cu:180-231): a[v] = |q| | sign << 31.
-    uint32_t a[32];
+    // Quantize (cu:180-231) into the row layout of kvszp_bits.h: P[k] holds
+    // the low fields ((|q| << 1) | sign) of elements k^7 and 16+(k^7).
+    uint32_t P[16];
     uint32_t orv = 0;
-    if (count == kBlockElems) {
-#pragma unroll
-        for (int v = 0; v < 32; ++v) {
-            const float x = (v & 1) ? bf16_hi(d[v >> 1]) : bf16_lo(d[v >> 1]);
-            const int32_t q = quantize<kQuant>(x, recip);
-            const uint32_t m = (uint32_t)(q < 0 ? -q : q);
-            orv |= m;
-            a[v] = m | ((uint32_t)q & 0x80000000u);
-        }
-    } else {
-#pragma unroll
-        for (int v = 0; v < 32; ++v) {
-            const float x = (v & 1) ? bf16_hi(d[v >> 1]) : bf16_lo(d[v >> 1]);
-            int32_t q = quantize<kQuant>(x, recip);
-            q = (uint32_t)v < count ? q : 0;
-            const uint32_t m = (uint32_t)(q < 0 ? -q : q);
-            orv |= m;
-            a[v] = m | ((uint32_t)q & 0x80000000u);
-        }
-    }
+    if (count == kBlockElems)
+        build_rows_lo<kQuant, true>(d, count, recip, P, orv);
+    else
+        build_rows_lo<kQuant, false>(d, count, recip, P, orv);
     const uint32_t rate = orv ? 32u - (uint32_t)__builtin_clz(orv) : 0u;
     const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
     s_rate[tid] = (uint8_t)rate;
@@ -576,14 +685,22 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     if (rmax == 0) return;
     uint32_t* dst = reinterpret_cast<uint32_t*>(J.out + R + s_prefix + sc.exclusive);
     const uint32_t count_words = rate ? rate + 1u : 0u;
-    if (rmax <= 15u) {
-        uint32_t words[16];
-        pack_block_words_narrow(a, words);
-        store_words<16>(dst, words, count_words, rmax + 1u);
-    } else {
-        uint32_t words[32];
-        pack_block_words_wide(a, words);
-        store_words<32>(dst, words, count_words, rmax + 1u);
+    transpose16x2(P);  // rows 0..15 = words w_0..w_15
+    store_words<16>(dst, P, count_words < 16u ? count_words : 16u,
+                    rmax < 15u ? rmax + 1u : 16u);
+    if (rmax >= 16u) {
+        // Planes 15..30 (rates 16..31): high fields, a second transpose.
+        // Rare, so the block is re-read instead of kept in registers.
+        uint32_t bad2 = 0;
+        load_block(g, J.in, tile_first, (uint32_t)tid * kBlockElems, count,
+                   p.aligned16 != 0, d, &bad2);
+        if (count == kBlockElems)
+            build_rows_hi<kQuant, true>(d, count, recip, P);
+        else
+            build_rows_hi<kQuant, false>(d, count, recip, P);
+        transpose16x2(P);
+        store_words<16>(dst + 16, P, count_words > 16u ? count_words - 16u : 0u,
+                        rmax - 15u);
     }
 }
 
@@ -601,7 +718,7 @@ __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
     const uint32_t job_in_group = local / g.tiles_per_job;
     const uint32_t tile = local - job_in_group * g.tiles_per_job;
     const uint32_t job = g.first_job + job_in_group;
-    const CompressJob J = p.jobs[job];
+    const CompressJob J = load_const(p.jobs, job);
     const uint64_t n = g.n;
     const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
     const uint32_t b = tile * kTileBlocks + tid;
@@ -657,13 +774,66 @@ __device__ __forceinline__ void store_block(uint16_t* dst, const uint32_t* out,
             v.y = out[4 * i + 1];
             v.z = out[4 * i + 2];
             v.w = out[4 * i + 3];
-            __builtin_nontemporal_store(v, p + i);
+            p[i] = v;
         }
         return;
     }
     __attribute__((address_space(1))) uint16_t* g = to_global(dst);
     for (uint32_t v = 0; v < count; ++v)
         g[v] = (uint16_t)((v & 1) ? (out[v >> 1] >> 16) : (out[v >> 1] & 0xFFFFu));
+}
+
+// Decodes one block payload (count words at src) into 16 packed BF16 pairs
+// (cu:496-538): words -> fields by the transpose, then
+// y = bf16_rne((float(q) * eb) * 2).  kWide: rates above 15, whose planes
+// 15..30 come from a second transpose of words 16..31.
+//
+// The wide path parks the high fields in LDS (`park`, one column per thread)
+// so that only one set of 16 rows is held in registers at a time.
+template <bool kWide>
+__device__ __forceinline__ void decode_words(const uint32_t* src,
+                                             uint32_t count_words, uint32_t rmax,
+                                             float eb, uint32_t rate,
+                                             uint32_t* out,
+                                             uint32_t (*park)[kThreads]) {
+    const int tid = threadIdx.x;
+    if (kWide) {
+        uint32_t H[16];
+        load_words<16>(src + 16, H, count_words > 16u ? count_words - 16u : 0u,
+                       rmax - 15u);
+        transpose16x2(H);  // H[k]: |q| >> 15 of elements k^7, 16+(k^7)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) park[k][tid] = H[k];
+        // Keep the compiler from forwarding the parked rows in registers.
+        __asm__ volatile("" ::: "memory");
+    }
+    uint32_t L[16];
+    load_words<16>(src, L, count_words < 16u ? count_words : 16u,
+                   rmax < 15u ? rmax + 1u : 16u);
+    transpose16x2(L);  // L[k]: low fields of elements k^7, 16+(k^7)
+    // out[i] holds elements 2i and 2i+1.  Rows k0, k1 feed both out[j]
+    // (low halves) and out[j + 8] (high halves), so they are consumed
+    // together.
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+        const int i = (n >> 1) + ((n & 1) ? 8 : 0);
+        const int v0 = 2 * i, v1 = 2 * i + 1;
+        const int k0 = (v0 & 15) ^ 7, k1 = (v1 & 15) ^ 7;
+        const int sh0 = v0 < 16 ? 0 : 16, sh1 = v1 < 16 ? 0 : 16;
+        const uint32_t lo0 = (L[k0] >> sh0) & 0xFFFFu, lo1 = (L[k1] >> sh1) & 0xFFFFu;
+        uint32_t m0 = lo0 >> 1, m1 = lo1 >> 1;
+        if (kWide) {
+            m0 |= ((park[k0][tid] >> sh0) & 0xFFFFu) << 15;
+            m1 |= ((park[k1][tid] >> sh1) & 0xFFFFu) << 15;
+        }
+        const int32_t q0 = (lo0 & 1u) ? -(int32_t)m0 : (int32_t)m0;
+        const int32_t q1 = (lo1 & 1u) ? -(int32_t)m1 : (int32_t)m1;
+        f32x2 y;
+        y.x = ((float)q0 * eb) * 2.0f;
+        y.y = ((float)q1 * eb) * 2.0f;
+        const bf16x2 h = __builtin_convertvector(y, bf16x2);
+        out[i] = rate ? __builtin_bit_cast(uint32_t, h) : 0u;
+    }
 }
 
 template <int kDst>
@@ -673,23 +843,22 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     __shared__ uint32_t s_wave[kThreads / 64];
     __shared__ uint32_t s_prefix;
     __shared__ uint32_t s_hdr[kTileBlocks / 4];
+    __shared__ uint32_t s_park[16][kThreads];  // wide-rate decode scratch
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    if (tid == 0) s_tile = take_ticket(p.ticket, p.ticket_base);
-    __syncthreads();
-    const uint32_t t = s_tile;
+    const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {
         if (tid == 0) flag_error(p.error, kErrSpin);
         return;
     }
     const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
     const uint32_t local = t - g.first_tile;
-    const uint32_t job_in_group = local / g.tiles_per_job;
+    const uint32_t job_in_group = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
     const uint32_t tile = local - job_in_group * g.tiles_per_job;
     const uint32_t job = g.first_job + job_in_group;
-    const DecompressJob J = p.jobs[job];
+    const DecompressJob J = load_const(p.jobs, job);
     const uint64_t n = g.n;
     const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
     const uint32_t b = tile * kTileBlocks + tid;
@@ -722,7 +891,8 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
         rate = 0;
     }
 
-    // Unpack (cu:496-538): rows-by-plane -> rows-by-element.
+    // Unpack (cu:496-538): stream words back to fields, then values
+    // y = bf16_rne((float(q) * eb) * 2) (cu:535-538).
     const uint32_t rmax = wave_max(rate);
     uint32_t out[16];
     if (rmax == 0) {
@@ -731,51 +901,10 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     } else {
         const uint32_t* src = reinterpret_cast<const uint32_t*>(J.in + base);
         const uint32_t count_words = rate ? rate + 1u : 0u;
-        uint32_t m[32];
-        const float eb = J.eb;
-        if (rmax <= 15u) {
-            uint32_t w[16];
-            load_words<16>(src, w, count_words, rmax + 1u);
-#pragma unroll
-            for (int i = 0; i < 15; ++i) m[i] = w[1 + i];
-            m[15] = w[0];
-            transpose16x2(m);
-#pragma unroll
-            for (int v = 0; v < 32; v += 2) {
-                const uint32_t f0 = v < 16 ? (m[v ^ 7] & 0xFFFFu) : (m[(v - 16) ^ 7] >> 16);
-                const uint32_t f1 = (v + 1) < 16 ? (m[(v + 1) ^ 7] & 0xFFFFu)
-                                                 : (m[(v + 1 - 16) ^ 7] >> 16);
-                const int32_t q0 = (f0 & 0x8000u) ? -(int32_t)(f0 & 0x7FFFu) : (int32_t)(f0 & 0x7FFFu);
-                const int32_t q1 = (f1 & 0x8000u) ? -(int32_t)(f1 & 0x7FFFu) : (int32_t)(f1 & 0x7FFFu);
-                f32x2 y;
-                y.x = ((float)q0 * eb) * 2.0f;
-                y.y = ((float)q1 * eb) * 2.0f;
-                const bf16x2 h = __builtin_convertvector(y, bf16x2);
-                out[v >> 1] = __builtin_bit_cast(uint32_t, h);
-            }
-        } else {
-            uint32_t w[32];
-            load_words<32>(src, w, count_words, rmax + 1u);
-#pragma unroll
-            for (int i = 0; i < 31; ++i) m[i] = w[1 + i];
-            m[31] = w[0];
-            transpose32(m);
-#pragma unroll
-            for (int v = 0; v < 32; v += 2) {
-                const uint32_t a0 = m[v ^ 7], a1 = m[(v + 1) ^ 7];
-                const int32_t q0 = (a0 >> 31) ? -(int32_t)(a0 & 0x7FFFFFFFu) : (int32_t)(a0 & 0x7FFFFFFFu);
-                const int32_t q1 = (a1 >> 31) ? -(int32_t)(a1 & 0x7FFFFFFFu) : (int32_t)(a1 & 0x7FFFFFFFu);
-                f32x2 y;
-                y.x = ((float)q0 * eb) * 2.0f;
-                y.y = ((float)q1 * eb) * 2.0f;
-                const bf16x2 h = __builtin_convertvector(y, bf16x2);
-                out[v >> 1] = __builtin_bit_cast(uint32_t, h);
-            }
-        }
-        if (rate == 0) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) out[i] = 0;
-        }
+        if (rmax <= 15u)
+            decode_words<false>(src, count_words, rmax, J.eb, rate, out, s_park);
+        else
+            decode_words<true>(src, count_words, rmax, J.eb, rate, out, s_park);
     }
 
     if (count && (rate != 0 || p.rate0_zero)) {
