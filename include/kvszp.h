@@ -15,7 +15,7 @@
  *  - `stream` is a hipStream_t (0 = legacy default stream).  Compress entry
  *    points block until sizes are on the host (the reference synchronizes,
  *    cuszp_wrapper.cpp:530); decompress entry points only enqueue
- *    (cuszp_wrapper.cpp:1102-1109).
+ *    (cuszp_wrapper.cpp:1102-1109).  kvszp_destroy waits for the device.
  *  - A context owns grow-only device workspaces, so one context must not be
  *    used from two host threads or two streams at once (same as the
  *    reference's CuSZpWrapper).
@@ -163,15 +163,22 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter(
  * counterpart: the reference's decoders have no device-side checks. */
 int kvszp_synchronize(kvszp_ctx* ctx, kvszp_stream_t stream);
 
-/* Kernel timing.  When enabled, every launch of this context is bracketed
- * by HIP events recorded on the launch stream (compress: relative-bound
- * pre-pass, if any, plus encoder; decompress: decoder).  kvszp_drain_timing
- * waits for the recorded events, returns the summed milliseconds and launch
- * counts per kind, and forgets them.  No reference counterpart: the
- * reference times whole stages with synchronize + perf_counter
- * (vllm_v1_compressed_offload.py:2009-2019). */
+/* Kernel timing.  For the kernel kinds in `kinds` (a mask of KVSZP_TIME_*;
+ * 0 disables), every launch of this context is bracketed by HIP events
+ * recorded on the launch stream (compress: relative-bound pre-pass, if any,
+ * plus encoder; decompress: decoder).  Each event record costs a few
+ * microseconds of GPU time, so time only the kind being measured.
+ * kvszp_drain_timing waits for the recorded events, returns the summed
+ * milliseconds and launch counts per kind, and forgets them.  No reference
+ * counterpart: the reference times whole stages with synchronize +
+ * perf_counter (vllm_v1_compressed_offload.py:2009-2019). */
 enum { KVSZP_KERNEL_COMPRESS = 0, KVSZP_KERNEL_DECOMPRESS = 1 };
-int kvszp_enable_timing(kvszp_ctx* ctx, int enable);
+enum {
+    KVSZP_TIME_COMPRESS = 1 << KVSZP_KERNEL_COMPRESS,
+    KVSZP_TIME_DECOMPRESS = 1 << KVSZP_KERNEL_DECOMPRESS,
+    KVSZP_TIME_ALL = KVSZP_TIME_COMPRESS | KVSZP_TIME_DECOMPRESS
+};
+int kvszp_enable_timing(kvszp_ctx* ctx, int kinds);
 int kvszp_drain_timing(kvszp_ctx* ctx, double* compress_ms, int* compress_count,
                        double* decompress_ms, int* decompress_count);
 

@@ -6,9 +6,11 @@
 //  - one launch per call, also for grouped requests (the reference launches
 //    once per group, cuszp_wrapper.cpp:795-848);
 //  - no per-call memsets: cross-workgroup words carry an epoch tag;
-//  - one H2D copy of a packed job table from a pinned staging ring, and one
-//    D2H copy of all sizes (the reference issues one D2H per page,
-//    cuszp_wrapper.cpp:523-529).
+//  - one H2D copy of a packed job table from a pinned staging ring; the
+//    encoder writes sizes and bounds straight into pinned host memory (the
+//    reference issues one D2H copy per page, cuszp_wrapper.cpp:523-529);
+//  - kernels raise a marker in a pinned host control block when they flag an
+//    error, so the device error word is copied back only when it is set.
 #include "kvszp.h"
 #include "kvszp_internal.h"
 
@@ -47,10 +49,14 @@ struct DevBuf {
     size_t bytes = 0;
 };
 
+// A pinned buffer the job table is copied from.  `seq` is the launch that
+// follows the copy: once that launch has published its sequence number the
+// copy has completed and the slot may be rewritten.
 struct StagingSlot {
     void* host = nullptr;
     size_t bytes = 0;
-    hipEvent_t done = nullptr;
+    uint32_t seq = 0;
+    hipStream_t stream = nullptr;
     bool pending = false;
 };
 
@@ -85,13 +91,16 @@ struct kvszp_ctx {
     unsigned long long* control = nullptr;
     unsigned long long ticket_next = 0;
     uint32_t epoch = 0;
-    DevBuf tile_state, tile_minmax, job_minmax, tables, results;
+    DevBuf tile_state, tile_minmax, job_minmax, tables;
     StagingSlot slots[kSlots];
     int next_slot = 0;
-    void* host_results = nullptr;
+    uint32_t seq = 0;                     // last launch sequence number
+    uint32_t* host_ctl = nullptr;         // pinned coherent control block
+    void* host_results = nullptr;         // pinned coherent sizes + bounds
     size_t host_results_bytes = 0;
-    // Optional kernel timing: event pairs recorded on the launch stream.
-    bool timing = false;
+    // Optional kernel timing: event pairs recorded on the launch stream for
+    // the kernel kinds in the mask (bit KVSZP_KERNEL_*).
+    int timing = 0;
     std::vector<TimingRecord> timed;      // recorded, not yet drained
     std::vector<hipEvent_t> spare_events;
 };
@@ -139,20 +148,28 @@ int ensure(DevBuf& b, size_t bytes, bool zero, hipStream_t stream) {
     return KVSZP_OK;
 }
 
+// Grows the pinned results area.  Only the encoder writes it and every
+// compress call waits for its kernel, so no launch still refers to the old
+// area when it is freed.
 int ensure_host_results(kvszp_ctx* c, size_t bytes) {
     if (bytes <= c->host_results_bytes) return KVSZP_OK;
     if (c->host_results) (void)hipHostFree(c->host_results);
     c->host_results = nullptr;
     c->host_results_bytes = 0;
     const size_t grown = std::max<size_t>(bytes, 4096);
-    hipError_t e = hipHostMalloc(&c->host_results, grown, hipHostMallocDefault);
+    hipError_t e = hipHostMalloc(&c->host_results, grown, hipHostMallocCoherent);
     if (e != hipSuccess) return fail(KVSZP_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
     c->host_results_bytes = grown;
     return KVSZP_OK;
 }
 
-// Copies `bytes` of host data to c->tables through a pinned staging slot.
-int upload_tables(kvszp_ctx* c, const void* data, size_t bytes,
+uint32_t host_seq(const kvszp_ctx* c) {
+    return __atomic_load_n(&c->host_ctl[kHostSeq], __ATOMIC_ACQUIRE);
+}
+
+// Copies `bytes` of host data to c->tables through a pinned staging slot;
+// `seq` is the sequence number of the launch that will read the table.
+int upload_tables(kvszp_ctx* c, const void* data, size_t bytes, uint32_t seq,
                   hipStream_t stream) {
     int rc = ensure(c->tables, bytes, false, stream);
     if (rc) return rc;
@@ -160,8 +177,13 @@ int upload_tables(kvszp_ctx* c, const void* data, size_t bytes,
     c->next_slot = (c->next_slot + 1) % kSlots;
     hipError_t e;
     if (s.pending) {
-        e = hipEventSynchronize(s.done);
-        if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+        // The copy out of this slot may still be queued: wait for it unless
+        // the launch behind it has already started.
+        if ((int32_t)(host_seq(c) - s.seq) < 0) {
+            e = s.stream == stream ? hipStreamSynchronize(stream)
+                                   : hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_fail(e, "synchronize (staging slot)");
+        }
         s.pending = false;
     }
     if (bytes > s.bytes) {
@@ -177,8 +199,8 @@ int upload_tables(kvszp_ctx* c, const void* data, size_t bytes,
     std::memcpy(s.host, data, bytes);
     e = hipMemcpyAsync(c->tables.ptr, s.host, bytes, hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D tables)");
-    e = hipEventRecord(s.done, stream);
-    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+    s.seq = seq;
+    s.stream = stream;
     s.pending = true;
     return KVSZP_OK;
 }
@@ -223,7 +245,7 @@ hipEvent_t take_event(kvszp_ctx* c) {
 // Starts a timed region on `stream` when timing is enabled; returns the index
 // of the record or -1.
 int timing_begin(kvszp_ctx* c, int kind, hipStream_t stream) {
-    if (!c->timing) return -1;
+    if (!(c->timing & (1 << kind))) return -1;
     TimingRecord r{kind, take_event(c), take_event(c), 0.0};
     if (!r.start || !r.stop || hipEventRecord(r.start, stream) != hipSuccess) {
         if (r.start) c->spare_events.push_back(r.start);
@@ -244,10 +266,20 @@ uint32_t header_bytes_of(uint64_t n) {
                       (kRefTileElems / kBlockElems));
 }
 
-// Reads (and clears) the device error word.  Caller has synchronized.
-int consume_device_error(kvszp_ctx* c, uint32_t err, hipStream_t stream) {
+// Reports (and clears) errors flagged by kernels of this context.  The
+// caller has synchronized `stream`, so no kernel of the context is running.
+// The device word is read only when a kernel raised the host marker.
+int consume_device_error(kvszp_ctx* c, hipStream_t stream) {
+    if (__atomic_load_n(&c->host_ctl[kHostErrorMarker], __ATOMIC_ACQUIRE) == 0)
+        return KVSZP_OK;
+    uint32_t err = 0;
+    hipError_t e = hipMemcpyAsync(&err, error_word(c), sizeof(err),
+                                  hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipMemsetAsync(error_word(c), 0, sizeof(uint32_t), stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return hip_fail(e, "reading the device error word");
+    __atomic_store_n(&c->host_ctl[kHostErrorMarker], 0u, __ATOMIC_RELEASE);
     if (!err) return KVSZP_OK;
-    (void)hipMemsetAsync(error_word(c), 0, sizeof(uint32_t), stream);
     std::string what;
     if (err & kErrSpin) what += " bounded-wait-expired";
     if (err & kErrLayerIndex) what += " layer-index-out-of-range";
@@ -355,16 +387,16 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     if ((rc = ensure(c->tile_state, total_tiles * 8, true, stream)) ||
         (rc = ensure(c->tile_minmax, total_tiles * 8, true, stream)) ||
         (rc = ensure(c->job_minmax, batch * 16, true, stream)) ||
-        (rc = ensure(c->results, batch * 8, false, stream)) ||
-        (rc = ensure_host_results(c, batch * 8 + 16)))
+        (rc = ensure_host_results(c, batch * 8)))
         return rc;
-    rc = upload_tables(c, jobs.data(), batch * sizeof(CompressJob), stream);
+    const uint32_t seq = ++c->seq;
+    rc = upload_tables(c, jobs.data(), batch * sizeof(CompressJob), seq, stream);
     if (rc) return rc;
     uint32_t epoch;
     if ((rc = next_epoch(c, stream, &epoch))) return rc;
 
-    uint32_t* job_size = reinterpret_cast<uint32_t*>(c->results.ptr);
-    float* job_eb = reinterpret_cast<float*>(job_size + batch);
+    uint32_t* host_sizes = reinterpret_cast<uint32_t*>(c->host_results);
+    float* host_bounds = reinterpret_cast<float*>(host_sizes + batch);
     const CompressJob* djobs = reinterpret_cast<const CompressJob*>(c->tables.ptr);
 
     hipError_t e;
@@ -375,6 +407,8 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         m.jobs = djobs;
         m.job_minmax = reinterpret_cast<unsigned long long*>(c->job_minmax.ptr);
         m.error = error_word(c);
+        m.host_ctl = c->host_ctl;
+        m.seq = seq;
         m.epoch = epoch;
         m.num_groups = (int)specs.size();
         std::memcpy(m.groups, p.groups, sizeof(m.groups));
@@ -385,9 +419,11 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
     p.tile_minmax = reinterpret_cast<unsigned long long*>(c->tile_minmax.ptr);
     p.job_minmax = reinterpret_cast<const unsigned long long*>(c->job_minmax.ptr);
-    p.job_size = job_size;
-    p.job_eb = job_eb;
+    p.host_sizes = host_sizes;
+    p.host_bounds = host_bounds;
     p.error = error_word(c);
+    p.host_ctl = c->host_ctl;
+    p.seq = seq;
     p.ticket = c->use_tickets ? c->control : nullptr;
     p.ticket_base = c->ticket_next;
     p.epoch = epoch;
@@ -401,27 +437,15 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     timing_end(c, rec, stream);
     c->ticket_next += total_tiles;
 
-    // One D2H of sizes (+ bounds) and the error word, then wait: callers need
-    // the sizes on the host (cuszp_wrapper.cpp:520-532).
-    char* host = reinterpret_cast<char*>(c->host_results);
-    const size_t result_bytes = batch * (relative ? 8 : 4);
-    e = hipMemcpyAsync(host + 16, c->results.ptr, result_bytes,
-                       hipMemcpyDeviceToHost, stream);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(D2H sizes)");
-    e = hipMemcpyAsync(host, error_word(c), sizeof(uint32_t),
-                       hipMemcpyDeviceToHost, stream);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(D2H error)");
+    // The encoder wrote sizes and bounds into pinned host memory; wait for it,
+    // since callers need the sizes on the host (cuszp_wrapper.cpp:520-532).
     e = hipStreamSynchronize(stream);
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    uint32_t err;
-    std::memcpy(&err, host, sizeof(err));
-    rc = consume_device_error(c, err, stream);
+    rc = consume_device_error(c, stream);
     if (rc) return rc;
-    const uint32_t* hs = reinterpret_cast<const uint32_t*>(host + 16);
-    const float* hb = reinterpret_cast<const float*>(hs + batch);
     for (size_t i = 0; i < batch; ++i) {
-        sizes_out[i] = hs[i];
-        bounds_out[i] = relative ? hb[i] : jobs[i].eps;
+        sizes_out[i] = host_sizes[i];
+        bounds_out[i] = relative ? host_bounds[i] : jobs[i].eps;
     }
     return KVSZP_OK;
 }
@@ -470,7 +494,8 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         std::memcpy(table.data() + jobs_bytes, dest_table.data(),
                     dest_table.size() * sizeof(uint16_t*));
     if ((rc = ensure(c->tile_state, total_tiles * 8, true, stream))) return rc;
-    if ((rc = upload_tables(c, table.data(), table.size(), stream))) return rc;
+    const uint32_t seq = ++c->seq;
+    if ((rc = upload_tables(c, table.data(), table.size(), seq, stream))) return rc;
     uint32_t epoch;
     if ((rc = next_epoch(c, stream, &epoch))) return rc;
 
@@ -481,6 +506,8 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         reinterpret_cast<char*>(c->tables.ptr) + jobs_bytes);
     p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
     p.error = error_word(c);
+    p.host_ctl = c->host_ctl;
+    p.seq = seq;
     p.ticket = c->use_tickets ? c->control : nullptr;
     p.ticket_base = c->ticket_next;
     p.epoch = epoch;
@@ -540,8 +567,10 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
     }
     e = hipMalloc(&c->control, 64);
     if (e == hipSuccess) e = hipMemset(c->control, 0, 64);
-    for (int i = 0; e == hipSuccess && i < kSlots; ++i)
-        e = hipEventCreateWithFlags(&c->slots[i].done, hipEventDisableTiming);
+    if (e == hipSuccess)
+        e = hipHostMalloc(reinterpret_cast<void**>(&c->host_ctl),
+                          kHostCtlWords * sizeof(uint32_t), hipHostMallocCoherent);
+    if (e == hipSuccess) std::memset(c->host_ctl, 0, kHostCtlWords * sizeof(uint32_t));
     if (e != hipSuccess) {
         kvszp_destroy(c);
         return hip_fail(e, "context setup");
@@ -558,24 +587,23 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
 int kvszp_destroy(kvszp_ctx* c) {
     if (!c) return KVSZP_OK;
     (void)hipSetDevice(c->device);
-    for (auto& s : c->slots) {
-        if (s.done) {
-            if (s.pending) (void)hipEventSynchronize(s.done);
-            (void)hipEventDestroy(s.done);
-        }
+    // Launches of this context may still be queued or running; they read the
+    // staging slots and write the host control block.
+    if (c->seq != 0) (void)hipDeviceSynchronize();
+    for (auto& s : c->slots)
         if (s.host) (void)hipHostFree(s.host);
-    }
     for (auto& r : c->timed) {
         (void)hipEventDestroy(r.start);
         (void)hipEventDestroy(r.stop);
     }
     for (hipEvent_t ev : c->spare_events) (void)hipEventDestroy(ev);
-    DevBuf* bufs[5] = {&c->tile_state, &c->tile_minmax, &c->job_minmax,
-                       &c->tables, &c->results};
+    DevBuf* bufs[4] = {&c->tile_state, &c->tile_minmax, &c->job_minmax,
+                       &c->tables};
     for (DevBuf* b : bufs)
         if (b->ptr) (void)hipFree(b->ptr);
     if (c->control) (void)hipFree(c->control);
     if (c->host_results) (void)hipHostFree(c->host_results);
+    if (c->host_ctl) (void)hipHostFree(c->host_ctl);
     delete c;
     return KVSZP_OK;
 }
@@ -771,20 +799,13 @@ int kvszp_synchronize(kvszp_ctx* c, kvszp_stream_t stream) {
     if (rc) return rc;
     hipError_t e = hipStreamSynchronize((hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    uint32_t err = 0;
-    e = hipMemcpy(&err, error_word(c), sizeof(err), hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpy(error word)");
-    rc = consume_device_error(c, err, (hipStream_t)stream);
-    if (rc) {
-        (void)hipStreamSynchronize((hipStream_t)stream);
-        return rc;
-    }
-    return KVSZP_OK;
+    return consume_device_error(c, (hipStream_t)stream);
 }
 
-int kvszp_enable_timing(kvszp_ctx* c, int enable) {
+int kvszp_enable_timing(kvszp_ctx* c, int kinds) {
     if (!c) return fail(KVSZP_EINVAL, "null context");
-    c->timing = enable != 0;
+    if (kinds & ~KVSZP_TIME_ALL) return fail(KVSZP_EINVAL, "unknown timing mask %d", kinds);
+    c->timing = kinds;
     return KVSZP_OK;
 }
 

@@ -60,6 +60,16 @@ struct Group {
     uint32_t header_bytes;      // R = 1024 * ceil(n / 32768)
 };
 
+// Host control block: pinned, coherent host memory that kernels write with
+// plain system-scope stores and the host reads after (or while) the stream
+// runs.  Word kHostErrorMarker becomes nonzero once any kernel flagged an
+// error (the bits themselves accumulate in the device error word);
+// word kHostSeq holds the sequence number of the last launch that started,
+// which tells the host that the table copy queued before it has completed.
+constexpr int kHostErrorMarker = 0;
+constexpr int kHostSeq = 1;
+constexpr int kHostCtlWords = 16;
+
 struct CompressJob {
     const uint16_t* in;         // BF16 page (full page when indexed)
     uint8_t* out;               // stream buffer, 4-byte aligned
@@ -79,9 +89,11 @@ struct CompressParams {
     unsigned long long* tile_state;   // look-back words, one per tile
     unsigned long long* tile_minmax;  // fused min/max words, one per tile
     const unsigned long long* job_minmax;  // pre-pass words, two per job
-    uint32_t* job_size;               // out: stream bytes per job
-    float* job_eb;                    // out: absolute bound per job
-    uint32_t* error;
+    uint32_t* host_sizes;             // out (pinned host): stream bytes per job
+    float* host_bounds;               // out (pinned host): absolute bound per job
+    uint32_t* error;                  // device error word (kErr* bits)
+    uint32_t* host_ctl;               // pinned host control words, see above
+    uint32_t seq;                     // launch sequence number
     unsigned long long* ticket;
     unsigned long long ticket_base;
     uint32_t epoch;
@@ -97,6 +109,8 @@ struct MinMaxParams {
     const CompressJob* jobs;
     unsigned long long* job_minmax;   // two words per job: max key, ~min key
     uint32_t* error;
+    uint32_t* host_ctl;
+    uint32_t seq;
     uint32_t epoch;
     uint32_t chunks_per_job;          // workgroups per job
     int num_groups;
@@ -108,6 +122,8 @@ struct DecompressParams {
     uint16_t* const* dests;           // kDstMulti destination table
     unsigned long long* tile_state;
     uint32_t* error;
+    uint32_t* host_ctl;
+    uint32_t seq;
     unsigned long long* ticket;
     unsigned long long ticket_base;
     uint32_t epoch;

@@ -67,8 +67,23 @@ __device__ __forceinline__ void store_relaxed(unsigned long long* p,
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void flag_error(uint32_t* e, uint32_t bits) {
+// Error reporting: the bits accumulate in the device word `e`; the host
+// control block gets a nonzero marker so the host learns of the error
+// without copying the device word back on every call.
+__device__ __forceinline__ void flag_error(uint32_t* e, uint32_t* host_ctl,
+                                           uint32_t bits) {
     __hip_atomic_fetch_or(e, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&host_ctl[kHostErrorMarker], 1u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// The first workgroup of a launch records the launch's sequence number in
+// the host control block: once it is visible, every copy queued on the
+// stream before this launch has completed.
+__device__ __forceinline__ void publish_seq(uint32_t* host_ctl, uint32_t seq) {
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(&host_ctl[kHostSeq], seq, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Tile number of this workgroup.  With a ticket counter the number is the
@@ -353,7 +368,7 @@ __device__ __forceinline__ TileScan tile_scan(uint32_t bytes, int tid,
 // Returns the exclusive prefix (bytes of earlier tiles of the job).
 __device__ uint32_t lookback(unsigned long long* state, uint32_t t,
                              uint32_t tile, uint32_t total, uint32_t epoch,
-                             uint32_t* err) {
+                             uint32_t* err, uint32_t* host_ctl) {
     const int lane = __lane_id();
     const uint32_t tag_agg = epoch * 4u + 1u;
     const uint32_t tag_inc = epoch * 4u + 2u;
@@ -383,7 +398,7 @@ __device__ uint32_t lookback(unsigned long long* state, uint32_t t,
             need = incl ? (((incl & (~incl + 1ull)) << 1) - 1ull) : win_mask;
             if ((ready & need) == need) break;
             if (spins >= kSpinLimit) {
-                if (lane == 0) flag_error(err, kErrSpin);
+                if (lane == 0) flag_error(err, host_ctl, kErrSpin);
                 need &= ready;
                 incl = 1;  // stop walking
                 break;
@@ -537,9 +552,10 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    publish_seq(p.host_ctl, p.seq);
     const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {  // tickets of another launch: never index past
-        if (tid == 0) flag_error(p.error, kErrSpin);
+        if (tid == 0) flag_error(p.error, p.host_ctl, kErrSpin);
         return;
     }
     const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
@@ -601,7 +617,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
                 unsigned long long w = load_relaxed(slot);
                 for (uint32_t spins = 0; (uint32_t)(w >> 32) != p.epoch; ++spins) {
                     if (spins >= kSpinLimit) {
-                        flag_error(p.error, kErrSpin);
+                        flag_error(p.error, p.host_ctl, kErrSpin);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);
@@ -669,15 +685,19 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
 
     if (wave == 0) {
         const uint32_t prefix =
-            lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error);
+            lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error, p.host_ctl);
         if (lane == 0) {
             s_prefix = prefix;
-            if (last_tile) p.job_size[job] = R + prefix + sc.total;
-            if (tile == 0) p.job_eb[job] = eb;
+            if (last_tile)
+                __hip_atomic_store(&p.host_sizes[job], R + prefix + sc.total,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (tile == 0)
+                __hip_atomic_store(&p.host_bounds[job], eb, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
-    if (bad & 1) flag_error(p.error, kErrLayerIndex);
-    if (bad & 2) flag_error(p.error, kErrSpin);
+    if (bad & 1) flag_error(p.error, p.host_ctl, kErrLayerIndex);
+    if (bad & 2) flag_error(p.error, p.host_ctl, kErrSpin);
     __syncthreads();
 
     // Payload (cu:302-358): sign word, then `rate` plane words.
@@ -712,6 +732,7 @@ __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    publish_seq(p.host_ctl, p.seq);
     const uint32_t t = blockIdx.x;
     const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
     const uint32_t local = t - g.first_tile;
@@ -757,7 +778,7 @@ __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
                                tag | (0xFFFFu - kmin), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (bad) flag_error(p.error, kErrLayerIndex);
+    if (bad) flag_error(p.error, p.host_ctl, kErrLayerIndex);
 }
 
 // ---- decoder ---------------------------------------------------------------
@@ -848,9 +869,10 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    publish_seq(p.host_ctl, p.seq);
     const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {
-        if (tid == 0) flag_error(p.error, kErrSpin);
+        if (tid == 0) flag_error(p.error, p.host_ctl, kErrSpin);
         return;
     }
     const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
@@ -881,7 +903,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     const TileScan sc = tile_scan(bytes, tid, s_wave);
     if (wave == 0) {
         const uint32_t prefix =
-            lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error);
+            lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error, p.host_ctl);
         if (lane == 0) s_prefix = prefix;
     }
     __syncthreads();
@@ -947,7 +969,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
             if (badl) err |= kErrLayerIndex;
         }
     }
-    if (err) flag_error(p.error, err);
+    if (err) flag_error(p.error, p.host_ctl, err);
 }
 
 }  // namespace

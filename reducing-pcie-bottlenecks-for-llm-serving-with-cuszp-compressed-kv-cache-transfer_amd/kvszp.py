@@ -30,6 +30,9 @@ MODE_FIXED, MODE_PLAIN, MODE_OUTLIER = 0, 1, 2
 TYPE_FLOAT, TYPE_DOUBLE = 0, 1
 QUANT_TWO_ROUNDINGS, QUANT_FUSED = 0, 1
 RATE0_SKIP, RATE0_ZERO = 0, 1
+KERNEL_COMPRESS, KERNEL_DECOMPRESS = 0, 1
+TIME_COMPRESS, TIME_DECOMPRESS = 1 << KERNEL_COMPRESS, 1 << KERNEL_DECOMPRESS
+TIME_ALL = TIME_COMPRESS | TIME_DECOMPRESS
 
 # (name, restype, argtypes) of every entry point declared in include/kvszp.h.
 _vp = ctypes.c_void_p
@@ -227,8 +230,12 @@ class Context:
     def synchronize(self, stream) -> int:
         return self._lib.kvszp_synchronize(self.handle, stream)
 
-    def enable_timing(self, enable: bool = True) -> None:
-        check(self._lib.kvszp_enable_timing(self.handle, int(enable)))
+    def enable_timing(self, kinds: int | bool = TIME_ALL) -> None:
+        """Times the launches of the kernel kinds in ``kinds`` (a mask of
+        TIME_*; True means all, False or 0 none)."""
+        if isinstance(kinds, bool):
+            kinds = TIME_ALL if kinds else 0
+        check(self._lib.kvszp_enable_timing(self.handle, int(kinds)))
 
     def drain_timing(self) -> dict:
         """Summed kernel milliseconds and launch counts since the last drain,
