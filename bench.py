@@ -200,6 +200,63 @@ def host_codec_baselines(w: Workload, max_pages: int) -> dict:
     return cpu_codecs.time_all(host)
 
 
+def _pmc_per_dispatch(run_dir: str, counter: str) -> dict:
+    """{kernel kind: [value per dispatch, KiB]} from a rocprofv3 --pmc CSV."""
+    import csv
+    from collections import defaultdict
+
+    path = os.path.join(run_dir, "run_counter_collection.csv")
+    per = defaultdict(float)
+    names = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != counter:
+                continue
+            did = int(row["Dispatch_Id"])
+            per[did] += float(row["Counter_Value"])
+            names[did] = row["Kernel_Name"]
+    out = defaultdict(list)
+    for did in sorted(per):
+        name = names[did]
+        if "compress_kernel" in name and "decompress" not in name:
+            kind = "compress_kernel"
+        elif "decompress_kernel" in name:
+            kind = "decompress_kernel"
+        elif "copyBuffer" in name:
+            kind = "copy"
+        else:
+            continue
+        out[kind].append(per[did])
+    return out
+
+
+def traffic_from(base: str) -> int:
+    """HBM bytes per launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch),
+    each scaled so that a plain device copy of known size reads and writes
+    exactly its own bytes."""
+    with open(os.path.join(base, "copy_calibration.json")) as f:
+        copy_bytes = json.load(f)["copy_bytes_each_way"]
+    cf = _pmc_per_dispatch(os.path.join(base, "copy_fetch"), "FETCH_SIZE")["copy"]
+    cw = _pmc_per_dispatch(os.path.join(base, "copy_write"), "WRITE_SIZE")["copy"]
+    fetch_factor = copy_bytes / (sum(cf) / len(cf) * 1024)
+    write_factor = copy_bytes / (sum(cw) / len(cw) * 1024)
+    bf = _pmc_per_dispatch(os.path.join(base, "bench_fetch"), "FETCH_SIZE")
+    bw = _pmc_per_dispatch(os.path.join(base, "bench_write"), "WRITE_SIZE")
+    result = {"fetch_factor": round(fetch_factor, 4),
+              "write_factor": round(write_factor, 4)}
+    for kind in ("compress_kernel", "decompress_kernel"):
+        fetch = sum(bf[kind]) / len(bf[kind]) * 1024 * fetch_factor
+        write = sum(bw[kind]) / len(bw[kind]) * 1024 * write_factor
+        result[kind] = int(round(fetch + write))
+        result[kind + "_fetch"] = int(round(fetch))
+        result[kind + "_write"] = int(round(write))
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(result, f, indent=1)
+    print(json.dumps(result))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -213,7 +270,13 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference "
                          "kernel for scaling rocprof FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--traffic-from", metavar="DIR",
+                    help="no GPU work: turn the rocprofv3 --pmc runs under DIR "
+                         "(copy_fetch, copy_write, bench_fetch, bench_write) into "
+                         "HBM bytes per launch, written to " + TRAFFIC_FILE)
     args = ap.parse_args()
+    if args.traffic_from:
+        return traffic_from(args.traffic_from)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(KV pages are private to the GPU that owns them; see DESIGN.md "

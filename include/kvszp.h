@@ -164,11 +164,11 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter(
 int kvszp_synchronize(kvszp_ctx* ctx, kvszp_stream_t stream);
 
 /* Kernel timing.  For the kernel kinds in `kinds` (a mask of KVSZP_TIME_*;
- * 0 disables), every launch of this context is bracketed by HIP events
- * recorded on the launch stream (compress: relative-bound pre-pass, if any,
- * plus encoder; decompress: decoder).  Each event record costs a few
- * microseconds of GPU time, so time only the kind being measured.
- * kvszp_drain_timing waits for the recorded events, returns the summed
+ * 0 disables), every launch of this context carries a pair of HIP events
+ * that the launch itself stamps with the kernel's start and end
+ * (hipExtLaunchKernelGGL; compress: relative-bound pre-pass, if any, plus
+ * encoder; decompress: decoder).  kvszp_drain_timing waits for the events,
+ * returns the summed
  * milliseconds and launch counts per kind, and forgets them.  No reference
  * counterpart: the reference times whole stages with synchronize +
  * perf_counter (vllm_v1_compressed_offload.py:2009-2019). */

@@ -242,12 +242,13 @@ hipEvent_t take_event(kvszp_ctx* c) {
     return e;
 }
 
-// Starts a timed region on `stream` when timing is enabled; returns the index
-// of the record or -1.
-int timing_begin(kvszp_ctx* c, int kind, hipStream_t stream) {
+// When timing is enabled for `kind`, returns the index of a new record whose
+// start/stop events the launch stamps with the kernel's own start and end;
+// otherwise -1.
+int timing_begin(kvszp_ctx* c, int kind) {
     if (!(c->timing & (1 << kind))) return -1;
     TimingRecord r{kind, take_event(c), take_event(c), 0.0};
-    if (!r.start || !r.stop || hipEventRecord(r.start, stream) != hipSuccess) {
+    if (!r.start || !r.stop) {
         if (r.start) c->spare_events.push_back(r.start);
         if (r.stop) c->spare_events.push_back(r.stop);
         return -1;
@@ -256,9 +257,11 @@ int timing_begin(kvszp_ctx* c, int kind, hipStream_t stream) {
     return (int)c->timed.size() - 1;
 }
 
-void timing_end(kvszp_ctx* c, int rec, hipStream_t stream) {
-    if (rec < 0) return;
-    (void)hipEventRecord(c->timed[rec].stop, stream);
+hipEvent_t timing_start(kvszp_ctx* c, int rec) {
+    return rec < 0 ? nullptr : c->timed[rec].start;
+}
+hipEvent_t timing_stop(kvszp_ctx* c, int rec) {
+    return rec < 0 ? nullptr : c->timed[rec].stop;
 }
 
 uint32_t header_bytes_of(uint64_t n) {
@@ -400,7 +403,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     const CompressJob* djobs = reinterpret_cast<const CompressJob*>(c->tables.ptr);
 
     hipError_t e;
-    const int rec = timing_begin(c, KVSZP_KERNEL_COMPRESS, stream);
+    const int rec = timing_begin(c, KVSZP_KERNEL_COMPRESS);
     if (bound_mode == kBoundPrepass) {
         MinMaxParams m;
         std::memset(&m, 0, sizeof(m));
@@ -412,7 +415,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         m.epoch = epoch;
         m.num_groups = (int)specs.size();
         std::memcpy(m.groups, p.groups, sizeof(m.groups));
-        e = launch_minmax(m, (uint32_t)total_tiles, stream);
+        e = launch_minmax(m, (uint32_t)total_tiles, stream, timing_start(c, rec));
         if (e != hipSuccess) return hip_fail(e, "minmax launch");
     }
     p.jobs = djobs;
@@ -432,9 +435,10 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     p.bound_mode = bound_mode;
     p.quantizer = c->quantizer;
     p.aligned16 = aligned16 ? 1 : 0;
-    e = launch_compress(p, stream);
+    e = launch_compress(p, stream,
+                        bound_mode == kBoundPrepass ? nullptr : timing_start(c, rec),
+                        timing_stop(c, rec));
     if (e != hipSuccess) return hip_fail(e, "compress launch");
-    timing_end(c, rec, stream);
     c->ticket_next += total_tiles;
 
     // The encoder wrote sizes and bounds into pinned host memory; wait for it,
@@ -528,10 +532,10 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     g.first_tile = 0;
     g.tiles_per_job = tiles_per_job;
     g.header_bytes = R;
-    const int rec = timing_begin(c, KVSZP_KERNEL_DECOMPRESS, stream);
-    hipError_t e = launch_decompress(p, stream);
+    const int rec = timing_begin(c, KVSZP_KERNEL_DECOMPRESS);
+    hipError_t e = launch_decompress(p, stream, timing_start(c, rec),
+                                     timing_stop(c, rec));
     if (e != hipSuccess) return hip_fail(e, "decompress launch");
-    timing_end(c, rec, stream);
     c->ticket_next += total_tiles;
     return KVSZP_OK;
 }

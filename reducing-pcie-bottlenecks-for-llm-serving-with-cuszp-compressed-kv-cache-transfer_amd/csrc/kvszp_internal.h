@@ -138,10 +138,13 @@ struct DecompressParams {
 };
 
 // Launchers (kvszp_kernels.hip).  Return hipGetLastError() of the launch.
-hipError_t launch_compress(const CompressParams& p, hipStream_t stream);
+// Non-null events are stamped with the kernel's start / end.
+hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
+                           hipEvent_t start, hipEvent_t stop);
 hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
-                         hipStream_t stream);
-hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream);
+                         hipStream_t stream, hipEvent_t start);
+hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
+                             hipEvent_t start, hipEvent_t stop);
 // Maximum co-resident workgroups of the compress kernel on this device.
 int compress_resident_workgroups(int device);
 

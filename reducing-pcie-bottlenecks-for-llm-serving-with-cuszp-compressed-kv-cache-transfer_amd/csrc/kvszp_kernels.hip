@@ -25,6 +25,8 @@
 
 #include <float.h>
 
+#include <hip/hip_ext.h>
+
 #pragma clang fp contract(off)
 
 namespace kvszp {
@@ -101,38 +103,56 @@ __device__ __forceinline__ uint32_t take_ticket(unsigned long long* ticket,
 
 // ---- wave / workgroup reductions ------------------------------------------
 
-__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+// Wave64 scans and reductions on DPP: row_shr:1,2,4,8 scan each row of 16
+// lanes, then row_bcast:15 and row_bcast:31 carry row totals into the rows
+// above.  A lane with no source lane keeps `identity`.  All 64 lanes must be
+// active.
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114,
+              kDppRowShr8 = 0x118, kDppRowBcast15 = 0x142,
+              kDppRowBcast31 = 0x143;
+
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t identity, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, kCtrl,
+                                                 kRowMask, 0xF, false);
+}
+
+template <class Op>
+__device__ __forceinline__ uint32_t wave_scan(uint32_t v, uint32_t identity,
+                                              Op op) {
+    v = op(v, dpp_move<kDppRowShr1, 0xF>(identity, v));
+    v = op(v, dpp_move<kDppRowShr2, 0xF>(identity, v));
+    v = op(v, dpp_move<kDppRowShr4, 0xF>(identity, v));
+    v = op(v, dpp_move<kDppRowShr8, 0xF>(identity, v));
+    v = op(v, dpp_move<kDppRowBcast15, 0xA>(identity, v));
+    v = op(v, dpp_move<kDppRowBcast31, 0xC>(identity, v));
     return v;
+}
+
+struct OpAdd {
+    __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; }
+};
+struct OpMax {
+    __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
+};
+struct OpMin {
+    __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; }
+};
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+    return __builtin_amdgcn_readlane(wave_scan(v, 0u, OpAdd()), 63);
 }
 
 __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) {
-        const uint32_t o = __shfl_xor(v, d, 64);
-        v = o > v ? o : v;
-    }
-    return v;
+    return __builtin_amdgcn_readlane(wave_scan(v, 0u, OpMax()), 63);
 }
 
 __device__ __forceinline__ uint32_t wave_min(uint32_t v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) {
-        const uint32_t o = __shfl_xor(v, d, 64);
-        v = o < v ? o : v;
-    }
-    return v;
+    return __builtin_amdgcn_readlane(wave_scan(v, 0xFFFFFFFFu, OpMin()), 63);
 }
 
-__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v,
-                                                        int lane) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t o = __shfl_up(v, d, 64);
-        if (lane >= d) v += o;
-    }
-    return v;
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v, int) {
+    return wave_scan(v, 0u, OpAdd());
 }
 
 // ---- quantizer and BF16 helpers -------------------------------------------
@@ -181,6 +201,44 @@ __device__ __forceinline__ float min_key_value(uint32_t k) {
 }
 __device__ __forceinline__ float max_key_value(uint32_t k) {
     return k == kKeyEmptyMax ? -FLT_MAX : key_value(k);
+}
+
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Order keys (kKeyEmpty* when none) of the smallest and largest non-NaN
+// values among the first `count` values of a block, d[] holding BF16 pairs
+// (fminf/fmaxf skip NaN, cu:78-79).  A full block is done two values per
+// instruction on packed 16-bit keys; NaN keys fall outside [key(-inf),
+// key(+inf)] = [0x007F, 0xFF80], so a block holding a NaN (or a partial
+// block) is redone value by value.
+__device__ __forceinline__ void block_key_minmax(const uint32_t* d,
+                                                 uint32_t count,
+                                                 uint32_t& kmin,
+                                                 uint32_t& kmax) {
+    if (count == kBlockElems) {
+        u16x2 mn = {0xFFFFu, 0xFFFFu}, mx = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < kBlockElems / 2; ++i) {
+            // key = sign ? ~h : h | 0x8000, for both halves at once
+            const uint32_t neg = __builtin_bit_cast(
+                uint32_t, __builtin_bit_cast(s16x2, d[i]) >> (short)15);
+            const u16x2 k = __builtin_bit_cast(u16x2, d[i] ^ (neg | 0x80008000u));
+            mn = __builtin_elementwise_min(mn, k);
+            mx = __builtin_elementwise_max(mx, k);
+        }
+        kmin = mn.x < mn.y ? mn.x : mn.y;
+        kmax = mx.x > mx.y ? mx.x : mx.y;
+        if (kmin >= 0x007Fu && kmax <= 0xFF80u) return;
+    }
+    float lo = FLT_MAX, hi = -FLT_MAX;
+    for (uint32_t v = 0; v < count; ++v) {
+        const float x = (v & 1) ? bf16_hi(d[v >> 1]) : bf16_lo(d[v >> 1]);
+        lo = fminf(lo, x);
+        hi = fmaxf(hi, x);
+    }
+    kmin = lo == FLT_MAX ? kKeyEmptyMin : bf16_key(lo);
+    kmax = hi == -FLT_MAX ? kKeyEmptyMax : bf16_key(hi);
 }
 
 // eb = eps * fmaxf(max - min, 1e-6f), cu:128-131.
@@ -582,15 +640,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     if (p.bound_mode != kBoundAbsolute) {
         uint32_t kmin, kmax;
         if (p.bound_mode == kBoundFused) {
-            // min/max of this thread's values (fminf/fmaxf skip NaN, cu:78-79)
-            float lo = FLT_MAX, hi = -FLT_MAX;
-            for (uint32_t v = 0; v < count; ++v) {
-                const float x = (v & 1) ? bf16_hi(d[v >> 1]) : bf16_lo(d[v >> 1]);
-                lo = fminf(lo, x);
-                hi = fmaxf(hi, x);
-            }
-            kmin = lo == FLT_MAX ? kKeyEmptyMin : bf16_key(lo);
-            kmax = hi == -FLT_MAX ? kKeyEmptyMax : bf16_key(hi);
+            block_key_minmax(d, count, kmin, kmax);
             kmin = wave_min(kmin);
             kmax = wave_max(kmax);
             if (lane == 0) {
@@ -750,14 +800,8 @@ __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
     uint32_t d[16];
     load_block(g, J.in, (uint64_t)tile * kTileElems, (uint32_t)tid * kBlockElems,
                count, false, d, &bad);
-    float lo = FLT_MAX, hi = -FLT_MAX;
-    for (uint32_t v = 0; v < count; ++v) {
-        const float x = (v & 1) ? bf16_hi(d[v >> 1]) : bf16_lo(d[v >> 1]);
-        lo = fminf(lo, x);
-        hi = fmaxf(hi, x);
-    }
-    uint32_t kmin = lo == FLT_MAX ? kKeyEmptyMin : bf16_key(lo);
-    uint32_t kmax = hi == -FLT_MAX ? kKeyEmptyMax : bf16_key(hi);
+    uint32_t kmin, kmax;
+    block_key_minmax(d, count, kmin, kmax);
     kmin = wave_min(kmin);
     kmax = wave_max(kmax);
     if (lane == 0) {
@@ -974,35 +1018,44 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
 
 }  // namespace
 
-hipError_t launch_compress(const CompressParams& p, hipStream_t stream) {
-    if (p.quantizer)
-        hipLaunchKernelGGL(compress_kernel<1>, dim3(p.total_tiles), dim3(kThreads),
-                           0, stream, p);
+// Launchers.  With timing events, hipExtLaunchKernelGGL stamps them with
+// the kernel's own start and end (no separate marker packets).
+template <class... Args>
+static void launch(void (*kernel)(Args...), uint32_t grid, hipStream_t stream,
+                   hipEvent_t start, hipEvent_t stop, Args... args) {
+    if (start || stop)
+        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream,
+                              start, stop, 0, args...);
     else
-        hipLaunchKernelGGL(compress_kernel<0>, dim3(p.total_tiles), dim3(kThreads),
-                           0, stream, p);
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream, args...);
+}
+
+hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
+                           hipEvent_t start, hipEvent_t stop) {
+    if (p.quantizer)
+        launch(compress_kernel<1>, p.total_tiles, stream, start, stop, p);
+    else
+        launch(compress_kernel<0>, p.total_tiles, stream, start, stop, p);
     return hipGetLastError();
 }
 
 hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
-                         hipStream_t stream) {
-    hipLaunchKernelGGL(minmax_kernel, dim3(grid), dim3(kThreads), 0, stream, p);
+                         hipStream_t stream, hipEvent_t start) {
+    launch(minmax_kernel, grid, stream, start, nullptr, p);
     return hipGetLastError();
 }
 
-hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream) {
+hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
+                             hipEvent_t start, hipEvent_t stop) {
     switch (p.dst_kind) {
     case kDstMulti:
-        hipLaunchKernelGGL(decompress_kernel<kDstMulti>, dim3(p.total_tiles),
-                           dim3(kThreads), 0, stream, p);
+        launch(decompress_kernel<kDstMulti>, p.total_tiles, stream, start, stop, p);
         break;
     case kDstIndexed:
-        hipLaunchKernelGGL(decompress_kernel<kDstIndexed>, dim3(p.total_tiles),
-                           dim3(kThreads), 0, stream, p);
+        launch(decompress_kernel<kDstIndexed>, p.total_tiles, stream, start, stop, p);
         break;
     default:
-        hipLaunchKernelGGL(decompress_kernel<kDstLinear>, dim3(p.total_tiles),
-                           dim3(kThreads), 0, stream, p);
+        launch(decompress_kernel<kDstLinear>, p.total_tiles, stream, start, stop, p);
         break;
     }
     return hipGetLastError();
