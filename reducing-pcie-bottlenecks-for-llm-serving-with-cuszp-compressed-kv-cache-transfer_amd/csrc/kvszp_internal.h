@@ -24,6 +24,9 @@ constexpr int kThreads = kTileBlocks;               // one thread per block
 constexpr int kTileElems = kTileBlocks * kBlockElems;
 constexpr int kRefTileElems = 32768;                // header granularity
 constexpr int kMaxGroups = 16;
+// Decoder: tiles up to this index within a job sum earlier header bytes
+// directly instead of waiting in the look-back.
+constexpr uint32_t kDirectPrefixTiles = 32;
 constexpr uint32_t kSpinLimit = 1u << 20;           // bounded waits (~1 s)
 
 // Device-side error bits (OR-ed into the context's error word).

@@ -420,6 +420,14 @@ __device__ __forceinline__ TileScan tile_scan(uint32_t bytes, int tid,
     return r;
 }
 
+// Payload bytes announced by one header dword (four rate bytes r):
+// sum of (r ? 4 + 4r : 0) = 4 * (sum of r + number of nonzero r).
+__device__ __forceinline__ uint32_t header_word_bytes(uint32_t w) {
+    const uint32_t sum = __builtin_amdgcn_sad_u8(w, 0u, 0u);
+    const uint32_t nz = (((w & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | w) & 0x80808080u;
+    return 4u * (sum + (uint32_t)__builtin_popcount(nz));
+}
+
 // Executed by one full wave.  Publishes this tile's aggregate, walks back
 // over earlier tiles of the same job 64 at a time until it meets one whose
 // inclusive prefix is published, and publishes its own inclusive prefix.
@@ -907,6 +915,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     __shared__ uint32_t s_tile;
     __shared__ uint32_t s_wave[kThreads / 64];
     __shared__ uint32_t s_prefix;
+    __shared__ uint32_t s_pre[kThreads / 64];
     __shared__ uint32_t s_hdr[kTileBlocks / 4];
     __shared__ uint32_t s_park[16][kThreads];  // wide-rate decode scratch
 
@@ -944,14 +953,38 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
         rate = 0;
     }
     const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
-    const TileScan sc = tile_scan(bytes, tid, s_wave);
-    if (wave == 0) {
-        const uint32_t prefix =
-            lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error, p.host_ctl);
-        if (lane == 0) s_prefix = prefix;
+    // Offset of this tile's payload in the job's stream.  The first tiles
+    // of a job add up the rate bytes of all earlier blocks straight from the
+    // header (cu:410-470 re-derives offsets from the header too), so they
+    // wait for no other workgroup; later tiles use the decoupled look-back,
+    // which stops at the nearest tile that published its inclusive prefix.
+    const bool direct = tile <= kDirectPrefixTiles;
+    if (direct) {
+        uint32_t part = 0;
+        const uint32_t* hw = reinterpret_cast<const uint32_t*>(J.in);
+        for (uint32_t i = tid; i < tile * (kTileBlocks / 4); i += kThreads)
+            part += header_word_bytes(to_global(hw)[i]);
+        part = wave_sum(part);
+        if (lane == 0) s_pre[wave] = part;
     }
-    __syncthreads();
-    const uint64_t base = (uint64_t)R + s_prefix + sc.exclusive;
+    const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
+    uint32_t prefix;
+    if (direct) {
+        prefix = s_pre[0] + s_pre[1] + s_pre[2] + s_pre[3];
+        if (tid == 0 && g.tiles_per_job > kDirectPrefixTiles + 1)
+            store_relaxed(&p.tile_state[t],
+                          ((unsigned long long)(p.epoch * 4u + 2u) << 32) |
+                              (prefix + sc.total));
+    } else {
+        if (wave == 0) {
+            const uint32_t pf = lookback(p.tile_state, t, tile, sc.total,
+                                         p.epoch, p.error, p.host_ctl);
+            if (lane == 0) s_prefix = pf;
+        }
+        __syncthreads();
+        prefix = s_prefix;
+    }
+    const uint64_t base = (uint64_t)R + prefix + sc.exclusive;
     if (rate && base + bytes > J.size) {
         err |= kErrTruncated;
         rate = 0;

@@ -159,7 +159,9 @@ def _encode(cpp, w, pages, eps):
     return bufs, sizes, bounds
 
 
-@pytest.mark.parametrize("n", [32, 77, 8192, 36864, 229376])
+# 327683 and 1048576 elements: tiles past the decoder's direct-prefix range
+# take the look-back
+@pytest.mark.parametrize("n", [32, 77, 8192, 36864, 229376, 327683, 1048576])
 @pytest.mark.parametrize("rate0", [0, 1])
 def test_decompress_contiguous_matches_oracle(cpp, oracle, n, rate0):
     pages = rand_pages(3, n, seed=n + 1)
@@ -349,6 +351,14 @@ def test_long_page_uses_prepass_and_matches_oracle(cpp, oracle):
     assert ok
     assert_streams(oracle, u16(pages), n, [1e-4, 1e-5], True, bufs, sizes,
                    bounds)
+    out = torch.empty((2, n), dtype=torch.bfloat16, device=DEV)
+    assert w.decompress_batch_fixed_bf16(bufs, sizes, out, n, bounds)
+    assert w.synchronize()
+    got = u16(out)
+    for i in range(2):
+        want = oracle.decompress_contiguous(bufs[i][:sizes[i]].cpu().numpy(), n,
+                                            bounds[i])
+        assert np.array_equal(got[i], want), f"page {i}"
 
 
 # ---- repeated calls, workspace growth, shared state ------------------------------
