@@ -87,6 +87,9 @@ struct kvszp_ctx {
     int rate0 = KVSZP_RATE0_ZERO;
     uint32_t fused_tile_limit = 0;
     bool use_tickets = false;  // KVSZP_TICKETS=1: ticket-ordered tiles
+    // Persistent encoder grid (co-resident workgroups); 0 = one workgroup
+    // per tile (KVSZP_PERSISTENT=0, or ticket mode).
+    uint32_t pipelined_grid = 0;
     // control words: [0] ticket counter, [1] low 32 bits = error word
     unsigned long long* control = nullptr;
     unsigned long long ticket_next = 0;
@@ -327,6 +330,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     std::memset(&p, 0, sizeof(p));
     std::vector<CompressJob> jobs(batch);
     bool aligned16 = true;
+    bool whole_blocks = true;  // every block whole and inside one layer
     uint64_t total_tiles = 0;
     uint32_t max_tiles_per_job = 0;
     size_t job = 0;
@@ -348,6 +352,8 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         max_tiles_per_job = std::max(max_tiles_per_job, g.tiles_per_job);
         total_tiles += (uint64_t)g.tiles_per_job * s.jobs;
         if (s.layers && (s.epl % 8) != 0) aligned16 = false;
+        if ((s.n % kBlockElems) != 0 || (s.layers && (s.epl % kBlockElems) != 0))
+            whole_blocks = false;
         // cuszp_wrapper.cpp:449-450 asks for capacity >= estimate(4n) = 8n.
         // That does not cover the header of tiny segments (R = 1024 bytes for
         // n < 128), so the worst-case stream R + 128 * nb is required too.
@@ -435,9 +441,20 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     p.bound_mode = bound_mode;
     p.quantizer = c->quantizer;
     p.aligned16 = aligned16 ? 1 : 0;
-    e = launch_compress(p, stream,
-                        bound_mode == kBoundPrepass ? nullptr : timing_start(c, rec),
-                        timing_stop(c, rec));
+    if (bound_mode != kBoundPrepass && c->pipelined_grid != 0 && whole_blocks &&
+        aligned16 && max_tiles_per_job <= c->pipelined_grid / 2) {
+        // Persistent encoder (whole, aligned, single-layer blocks only); its
+        // waits are cycle-free while a job's tiles number at most the grid
+        // (half of it here, for margin).
+        p.ticket = nullptr;
+        const uint32_t grid = (uint32_t)std::min<uint64_t>(total_tiles, c->pipelined_grid);
+        e = launch_compress_pipelined(p, grid, stream, timing_start(c, rec),
+                                      timing_stop(c, rec));
+    } else {
+        e = launch_compress(p, stream,
+                            bound_mode == kBoundPrepass ? nullptr : timing_start(c, rec),
+                            timing_stop(c, rec));
+    }
     if (e != hipSuccess) return hip_fail(e, "compress launch");
     c->ticket_next += total_tiles;
 
@@ -582,8 +599,18 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
     // Tiles of one job wait for each other in the fused relative-bound
     // exchange, so a job may use it only if all its tiles fit on the device
     // at once with a wide margin.
-    const int resident = compress_resident_workgroups(device_id);
+    const int resident = compress_resident_workgroups(device_id, false);
     c->fused_tile_limit = (uint32_t)std::min(kThreads, std::max(0, resident / 4));
+    {
+        const char* env = std::getenv("KVSZP_PERSISTENT");
+        const bool off = (env && env[0] == '0') || c->use_tickets;
+        c->pipelined_grid =
+            off ? 0u : (uint32_t)std::max(0, compress_resident_workgroups(device_id, true));
+    }
+    if (const char* dbg = std::getenv("KVSZP_DEBUG"); dbg && dbg[0] == '1')
+        std::fprintf(stderr, "kvszp: device %d resident encoder workgroups %d, "
+                     "fused tile limit %u, persistent grid %u\n", device_id,
+                     resident, c->fused_tile_limit, c->pipelined_grid);
     *out = c;
     return KVSZP_OK;
 }

@@ -144,12 +144,16 @@ struct DecompressParams {
 // Non-null events are stamped with the kernel's start / end.
 hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
                            hipEvent_t start, hipEvent_t stop);
+// Persistent encoder: `grid` workgroups (all co-resident) walk the tiles.
+hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
+                                     hipStream_t stream, hipEvent_t start,
+                                     hipEvent_t stop);
 hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
                          hipStream_t stream, hipEvent_t start);
 hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
                              hipEvent_t start, hipEvent_t stop);
-// Maximum co-resident workgroups of the compress kernel on this device.
-int compress_resident_workgroups(int device);
+// Maximum co-resident workgroups of an encoder kernel on this device.
+int compress_resident_workgroups(int device, bool pipelined);
 
 }  // namespace kvszp
 

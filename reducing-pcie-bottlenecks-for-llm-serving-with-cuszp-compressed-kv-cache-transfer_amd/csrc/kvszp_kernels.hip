@@ -428,24 +428,31 @@ __device__ __forceinline__ uint32_t header_word_bytes(uint32_t w) {
     return 4u * (sum + (uint32_t)__builtin_popcount(nz));
 }
 
-// Executed by one full wave.  Publishes this tile's aggregate, walks back
-// over earlier tiles of the same job 64 at a time until it meets one whose
-// inclusive prefix is published, and publishes its own inclusive prefix.
-// Returns the exclusive prefix (bytes of earlier tiles of the job).
-__device__ uint32_t lookback(unsigned long long* state, uint32_t t,
-                             uint32_t tile, uint32_t total, uint32_t epoch,
-                             uint32_t* err, uint32_t* host_ctl) {
+// Decoupled look-back over the tiles of one job.  Tile state words carry
+// an epoch tag: epoch*4+1 = aggregate (this tile's bytes), epoch*4+2 =
+// inclusive prefix (bytes of this and all earlier tiles of the job).
+//
+// lookback_publish: lane 0 publishes the tile's aggregate (tile 0 its
+// inclusive prefix right away).
+__device__ __forceinline__ void lookback_publish(unsigned long long* state,
+                                                 uint32_t t, uint32_t tile,
+                                                 uint32_t total, uint32_t epoch) {
+    if (__lane_id() != 0) return;
+    const uint32_t tag = epoch * 4u + (tile == 0 ? 2u : 1u);
+    store_relaxed(&state[t], ((unsigned long long)tag << 32) | total);
+}
+
+// lookback_wait: executed by one full wave after lookback_publish.  Walks
+// back over earlier tiles of the job 64 at a time until it meets one whose
+// inclusive prefix is published, publishes this tile's inclusive prefix and
+// returns the exclusive one (bytes of earlier tiles of the job).
+__device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
+                                  uint32_t tile, uint32_t total, uint32_t epoch,
+                                  uint32_t* err, uint32_t* host_ctl) {
+    if (tile == 0) return 0;
     const int lane = __lane_id();
     const uint32_t tag_agg = epoch * 4u + 1u;
     const uint32_t tag_inc = epoch * 4u + 2u;
-    if (tile == 0) {
-        if (lane == 0)
-            store_relaxed(&state[t],
-                          ((unsigned long long)tag_inc << 32) | total);
-        return 0;
-    }
-    if (lane == 0)
-        store_relaxed(&state[t], ((unsigned long long)tag_agg << 32) | total);
     uint32_t acc = 0;
     uint32_t remaining = tile;   // earlier tiles of this job
     uint32_t pos = t - 1;        // tile read by lane 0
@@ -480,6 +487,15 @@ __device__ uint32_t lookback(unsigned long long* state, uint32_t t,
         store_relaxed(&state[t],
                       ((unsigned long long)tag_inc << 32) | (acc + total));
     return acc;
+}
+
+// Both halves back to back (one full wave).
+__device__ __forceinline__ uint32_t lookback(unsigned long long* state,
+                                             uint32_t t, uint32_t tile,
+                                             uint32_t total, uint32_t epoch,
+                                             uint32_t* err, uint32_t* host_ctl) {
+    lookback_publish(state, t, tile, total, epoch);
+    return lookback_wait(state, t, tile, total, epoch, err, host_ctl);
 }
 
 // Finds the group of tile t (groups are few and ordered by first_tile).
@@ -588,6 +604,42 @@ __device__ __forceinline__ void build_rows_lo(const uint32_t* d, uint32_t count,
         const uint32_t m0 = magnitude(q0), m1 = magnitude(q1);
         orv |= m0 | m1;
         P[k] = field_lo(m0, (uint32_t)q0 >> 31) | (field_lo(m1, (uint32_t)q1 >> 31) << 16);
+    }
+}
+
+// build_rows_lo for a full block, one row after the other: each row's
+// reciprocal passes through an empty asm that takes the previous row as an
+// input, so the scheduler cannot start all 32 conversions at once (which
+// would hold ~2x the registers inside the persistent encoder's loop).
+template <int kQuant>
+__device__ __forceinline__ void build_rows_lo_chained(const uint32_t* d, float recip,
+                                                      uint32_t* P, uint32_t& orv) {
+    uint32_t prev = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        float r = recip;
+        asm volatile("" : "+v"(r) : "v"(prev));
+        const int32_t q0 = quant_elem<kQuant, true>(d, row_lo_elem(k), kBlockElems, r);
+        const int32_t q1 = quant_elem<kQuant, true>(d, row_hi_elem(k), kBlockElems, r);
+        const uint32_t m0 = magnitude(q0), m1 = magnitude(q1);
+        orv |= m0 | m1;
+        P[k] = field_lo(m0, (uint32_t)q0 >> 31) | (field_lo(m1, (uint32_t)q1 >> 31) << 16);
+        prev = P[k];
+    }
+}
+
+template <int kQuant>
+__device__ __forceinline__ void build_rows_hi_chained(const uint32_t* d, float recip,
+                                                      uint32_t* P) {
+    uint32_t prev = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        float r = recip;
+        asm volatile("" : "+v"(r) : "v"(prev));
+        const uint32_t m0 = magnitude(quant_elem<kQuant, true>(d, row_lo_elem(k), kBlockElems, r));
+        const uint32_t m1 = magnitude(quant_elem<kQuant, true>(d, row_hi_elem(k), kBlockElems, r));
+        P[k] = field_hi(m0) | (field_hi(m1) << 16);
+        prev = P[k];
     }
 }
 
@@ -780,6 +832,372 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
         store_words<16>(dst + 16, P, count_words > 16u ? count_words - 16u : 0u,
                         rmax - 15u);
     }
+}
+
+// ---- persistent, software-pipelined encoder --------------------------------
+//
+// For launches whose blocks are all whole, inside one layer and 16-byte
+// aligned (every segment length and layer length a multiple of 32 values,
+// every page 16-byte aligned) -- the shape of KV pages.  Workgroup w encodes
+// tiles w, w + G, w + 2G, ... (G = gridDim.x, at most the number of
+// co-resident workgroups).  While tile t waits on other tiles -- the
+// relative-bound exchange and the offset look-back -- the blocks of its next
+// tile are already on their way into LDS, and that tile's min/max is
+// published before this tile's look-back wait.  Per iteration:
+//   a. exchange: min/max of all tiles of t's job -> bound
+//   b. quantize t (registers) -> fields, rates
+//   c. tile scan, header bytes, publish t's aggregate
+//   d. next tile: min/max from its LDS copy, published
+//   e. look-back wait -> t's offset
+//   f. payload stores of t
+//   g. next tile's blocks LDS -> registers; start the copy of the one after
+// Every wait of tile t is on a publish that happens before any wait of a
+// lower "rank" (2t for a, 2t+1 for e) once tiles_per_job <= G, so with all G
+// workgroups resident no cycle of waits exists.  All waits are bounded.
+
+// threadIdx.x behind an empty asm: values derived from it inside the tile
+// loop are recomputed each iteration instead of being hoisted out of the
+// loop and held in registers for its whole length.
+__device__ __forceinline__ int loop_tid() {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// Per-tile uniform context.
+struct TileCtx {
+    uint32_t t;     // tile number in the launch
+    int gi;         // group
+    uint32_t job;   // job index
+    uint32_t tile;  // tile within the job
+    CompressJob J;
+};
+
+// Group lookup from first-tile numbers kept in LDS (a loop over kernel
+// arguments would keep all of them in scalar registers across the tile loop).
+__device__ __forceinline__ TileCtx tile_ctx(const CompressParams& p, uint32_t t,
+                                            const uint32_t* s_gfirst) {
+    TileCtx c;
+    c.t = t;
+    int gi = 0;
+    for (int i = 1; i < p.num_groups; ++i)
+        if (t >= s_gfirst[i]) gi = i;
+    c.gi = __builtin_amdgcn_readfirstlane(gi);
+    const Group& g = p.groups[c.gi];
+    const uint32_t local = t - g.first_tile;
+    const uint32_t jig = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
+    c.tile = local - jig * g.tiles_per_job;
+    c.job = g.first_job + jig;
+    c.J = load_const(p.jobs, c.job);
+    return c;
+}
+
+// Whether this thread's block exists (all existing blocks are whole here).
+__device__ __forceinline__ bool block_exists(const Group& g, uint32_t tile, int tid) {
+    return (uint64_t)(tile * kTileBlocks + tid) * kBlockElems < g.n;
+}
+
+// Source element of this thread's block.
+__device__ __forceinline__ uint64_t block_source(const Group& g, uint32_t tile,
+                                                 int tid, uint32_t* bad) {
+    const uint64_t tile_first = (uint64_t)tile * kTileElems;
+    const uint32_t elem = (uint32_t)tid * kBlockElems;
+    if (g.layers == nullptr) return tile_first + elem;
+    return layer_cursor(g, tile_first, elem, bad).src_index;
+}
+
+// Starts the asynchronous copy of this thread's block into the wave's LDS
+// slots: lane l's 16-byte chunk c lands at slot 64c + l.
+__device__ __forceinline__ void stage_block(const Group& g, const uint16_t* in,
+                                            uint32_t tile, uint32_t* lds_wave,
+                                            uint32_t* bad, int tid) {
+    if (!block_exists(g, tile, tid)) return;
+    const char* src = reinterpret_cast<const char*>(in + block_source(g, tile, tid, bad));
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(src + 16 * c),
+            (__attribute__((address_space(3))) void*)(lds_wave + 256 * c), 16, 0, 0);
+}
+
+// This thread's staged block, LDS -> registers (zeros if it does not exist).
+__device__ __forceinline__ void staged_block(const uint32_t* lds_wave, bool exists,
+                                             uint32_t* d, int tid) {
+    const u32x4* slots = reinterpret_cast<const u32x4*>(lds_wave);
+    const int lane = tid & 63;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u32x4 v = exists ? slots[64 * c + lane] : u32x4{0u, 0u, 0u, 0u};
+        d[4 * c + 0] = v.x;
+        d[4 * c + 1] = v.y;
+        d[4 * c + 2] = v.z;
+        d[4 * c + 3] = v.w;
+    }
+}
+
+// Min/max keys of this thread's staged block, 16 bytes at a time from LDS
+// (few registers while the current tile's fields are live).  A block
+// holding a NaN is redone value by value, skipping NaNs (cu:78-79).
+__device__ __forceinline__ void staged_block_minmax(const uint32_t* lds_wave,
+                                                    bool exists, int tid,
+                                                    uint32_t& kmin, uint32_t& kmax) {
+    kmin = kKeyEmptyMin;
+    kmax = kKeyEmptyMax;
+    if (!exists) return;
+    const u32x4* slots = reinterpret_cast<const u32x4*>(lds_wave);
+    const int lane = tid & 63;
+    u16x2 mn = {0xFFFFu, 0xFFFFu}, mx = {0u, 0u};
+#pragma unroll 1
+    for (int c = 0; c < 4; ++c) {
+        const u32x4 v = slots[64 * c + lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = v[i];
+            const uint32_t neg = __builtin_bit_cast(
+                uint32_t, __builtin_bit_cast(s16x2, w) >> (short)15);
+            const u16x2 k = __builtin_bit_cast(u16x2, w ^ (neg | 0x80008000u));
+            mn = __builtin_elementwise_min(mn, k);
+            mx = __builtin_elementwise_max(mx, k);
+        }
+    }
+    kmin = mn.x < mn.y ? mn.x : mn.y;
+    kmax = mx.x > mx.y ? mx.x : mx.y;
+    if (kmin >= 0x007Fu && kmax <= 0xFF80u) return;
+    const uint32_t* words = lds_wave;
+    float lo = FLT_MAX, hi = -FLT_MAX;
+#pragma unroll 1
+    for (int v = 0; v < kBlockElems; ++v) {
+        const uint32_t w = words[(64 * (v >> 3) + lane) * 4 + ((v >> 1) & 3)];
+        const float x = (v & 1) ? bf16_hi(w) : bf16_lo(w);
+        lo = fminf(lo, x);
+        hi = fmaxf(hi, x);
+    }
+    kmin = lo == FLT_MAX ? kKeyEmptyMin : bf16_key(lo);
+    kmax = hi == -FLT_MAX ? kKeyEmptyMax : bf16_key(hi);
+}
+
+// Tile min/max: this thread's keys -> the tile's epoch-tagged word (one
+// barrier).
+__device__ __forceinline__ void publish_tile_keys(const CompressParams& p,
+                                                  uint32_t t, uint32_t kmin,
+                                                  uint32_t kmax, uint32_t* s_min,
+                                                  uint32_t* s_max, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    kmin = wave_min(kmin);
+    kmax = wave_max(kmax);
+    if (lane == 0) {
+        s_min[wave] = kmin;
+        s_max[wave] = kmax;
+    }
+    __syncthreads();
+    if (tid == 0) {
+#pragma unroll
+        for (int w = 1; w < kThreads / 64; ++w) {
+            kmin = s_min[w] < kmin ? s_min[w] : kmin;
+            kmax = s_max[w] > kmax ? s_max[w] : kmax;
+        }
+        store_relaxed(&p.tile_minmax[t],
+                      ((unsigned long long)p.epoch << 32) | (kmin << 16) | kmax);
+    }
+}
+
+// Min/max keys over all tiles of the job (one barrier); thread i < tiles
+// polls tile i's word.
+__device__ __forceinline__ void exchange_minmax(const CompressParams& p,
+                                                uint32_t first_t, uint32_t tiles,
+                                                uint32_t* s_min, uint32_t* s_max,
+                                                uint32_t& kmin, uint32_t& kmax,
+                                                int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    kmin = kKeyEmptyMin;
+    kmax = kKeyEmptyMax;
+    if ((uint32_t)tid < tiles) {
+        const unsigned long long* slot = &p.tile_minmax[first_t + tid];
+        unsigned long long w = load_relaxed(slot);
+        for (uint32_t spins = 0; (uint32_t)(w >> 32) != p.epoch; ++spins) {
+            if (spins >= kSpinLimit) {
+                flag_error(p.error, p.host_ctl, kErrSpin);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            w = load_relaxed(slot);
+        }
+        kmin = (uint32_t)(w >> 16) & 0xFFFFu;
+        kmax = (uint32_t)w & 0xFFFFu;
+    }
+    kmin = wave_min(kmin);
+    kmax = wave_max(kmax);
+    if (lane == 0) {
+        s_min[wave] = kmin;
+        s_max[wave] = kmax;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+        kmin = s_min[w] < kmin ? s_min[w] : kmin;
+        kmax = s_max[w] > kmax ? s_max[w] : kmax;
+    }
+}
+
+// Six waves per SIMD: at 80 VGPRs the loop body needs no scratch (at 64 or 72
+// it spills, and measured slower than this).
+template <int kQuant>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(6, 6))) void compress_pipelined_kernel(
+    CompressParams p) {
+    __shared__ uint32_t s_wave[kThreads / 64];
+    __shared__ uint32_t s_min[kThreads / 64], s_max[kThreads / 64];    // publish
+    __shared__ uint32_t s_xmin[kThreads / 64], s_xmax[kThreads / 64];  // exchange
+    __shared__ uint32_t s_prefix;
+    __shared__ uint32_t s_gfirst[kMaxGroups];
+    __shared__ uint8_t s_rate[kTileBlocks];
+    __shared__ __attribute__((aligned(16))) uint32_t s_stage[kThreads / 64][1024];
+
+    publish_seq(p.host_ctl, p.seq);
+    if ((int)threadIdx.x < p.num_groups) s_gfirst[threadIdx.x] = p.groups[threadIdx.x].first_tile;
+    __syncthreads();
+    const uint32_t G = gridDim.x;
+    const bool fused = p.bound_mode == kBoundFused;
+    uint32_t bad = 0;
+
+    // Prologue: stage the first tile, publish its min/max, stage the next.
+    TileCtx cur = tile_ctx(p, blockIdx.x, s_gfirst);
+    uint32_t d[16];
+    bool has_next;
+    TileCtx nxt;
+    {
+        const int tid = loop_tid();
+        uint32_t* stage = &s_stage[tid >> 6][0];
+        const Group& g = p.groups[cur.gi];
+        const bool ex = block_exists(g, cur.tile, tid);
+        stage_block(g, cur.J.in, cur.tile, stage, &bad, tid);
+        __builtin_amdgcn_s_waitcnt(0);
+        staged_block(stage, ex, d, tid);
+        if (fused) {
+            uint32_t kmin, kmax;
+            block_key_minmax(d, ex ? kBlockElems : 0u, kmin, kmax);
+            publish_tile_keys(p, cur.t, kmin, kmax, s_min, s_max, tid);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // LDS reads done before it is refilled
+        has_next = cur.t + G < p.total_tiles;
+        if (has_next) {
+            nxt = tile_ctx(p, cur.t + G, s_gfirst);
+            stage_block(p.groups[nxt.gi], nxt.J.in, nxt.tile, stage, &bad, tid);
+        }
+    }
+
+    for (;;) {
+        const int tid = loop_tid();
+        const int lane = tid & 63;
+        const int wave = tid >> 6;
+        uint32_t* stage = &s_stage[wave][0];
+        const Group& g = p.groups[cur.gi];
+        const bool ex = block_exists(g, cur.tile, tid);
+
+        // a. bound
+        float eb = cur.J.eps;
+        if (fused) {
+            uint32_t kmin, kmax;
+            exchange_minmax(p, cur.t - cur.tile, g.tiles_per_job, s_xmin, s_xmax,
+                            kmin, kmax, tid);
+            eb = relative_bound(cur.J.eps, kmin, kmax);
+        }
+        const float recip = 0.5f / eb;  // cu:166, IEEE division
+
+        // b. quantize (cu:180-231); a block past the end has d = 0 -> rate 0
+        uint32_t P[16];
+        uint32_t orv = 0;
+        build_rows_lo_chained<kQuant>(d, recip, P, orv);
+        const uint32_t rate = (ex && orv) ? 32u - (uint32_t)__builtin_clz(orv) : 0u;
+        const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
+        s_rate[tid] = (uint8_t)rate;
+
+        // c. scan, header bytes (cu:226-229; padding zeroed by the last
+        // tile), aggregate out
+        const TileScan sc = tile_scan(bytes, tid, s_wave);
+        const uint32_t R = g.header_bytes;
+        if (tid < kTileBlocks / 4) {
+            const uint32_t word = (uint32_t)s_rate[4 * tid] |
+                                  ((uint32_t)s_rate[4 * tid + 1] << 8) |
+                                  ((uint32_t)s_rate[4 * tid + 2] << 16) |
+                                  ((uint32_t)s_rate[4 * tid + 3] << 24);
+            *to_global(reinterpret_cast<uint32_t*>(cur.J.out + cur.tile * kTileBlocks + 4 * tid)) = word;
+        }
+        const bool last_tile = cur.tile + 1 == g.tiles_per_job;
+        if (last_tile) {
+            for (uint32_t off = (cur.tile + 1) * kTileBlocks + 4u * tid; off < R;
+                 off += 4u * kThreads)
+                *to_global(reinterpret_cast<uint32_t*>(cur.J.out + off)) = 0u;
+        }
+        if (wave == 0) lookback_publish(p.tile_state, cur.t, cur.tile, sc.total, p.epoch);
+
+        // d. next tile's min/max while this tile's predecessors finish
+        if (has_next && fused) {
+            uint32_t kmin, kmax;
+            __builtin_amdgcn_s_waitcnt(0);  // staged LDS writes have landed
+            staged_block_minmax(stage, block_exists(p.groups[nxt.gi], nxt.tile, tid),
+                                tid, kmin, kmax);
+            publish_tile_keys(p, nxt.t, kmin, kmax, s_min, s_max, tid);
+        }
+
+        // e. offset
+        if (wave == 0) {
+            const uint32_t prefix = lookback_wait(p.tile_state, cur.t, cur.tile,
+                                                  sc.total, p.epoch, p.error,
+                                                  p.host_ctl);
+            if (lane == 0) {
+                s_prefix = prefix;
+                if (last_tile)
+                    __hip_atomic_store(&p.host_sizes[cur.job], R + prefix + sc.total,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (cur.tile == 0)
+                    __hip_atomic_store(&p.host_bounds[cur.job], eb, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+        __syncthreads();
+
+        // f. payload (cu:302-358)
+        const uint32_t rmax = wave_max(rate);
+        if (rmax != 0) {
+            uint32_t* dst = reinterpret_cast<uint32_t*>(cur.J.out + R + s_prefix + sc.exclusive);
+            const uint32_t count_words = rate ? rate + 1u : 0u;
+            transpose16x2(P);
+            store_words<16>(dst, P, count_words < 16u ? count_words : 16u,
+                            rmax < 15u ? rmax + 1u : 16u);
+            if (rmax >= 16u) {
+                // Planes 15..30 (rates 16..31): rare, so the block is re-read
+                // rather than kept in registers across the waits.
+                const g_u32x4* src = (const g_u32x4*)to_global(
+                    cur.J.in + (ex ? block_source(g, cur.tile, tid, &bad) : 0));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const u32x4 v = ex ? src[i] : u32x4{0u, 0u, 0u, 0u};
+                    d[4 * i + 0] = v.x;
+                    d[4 * i + 1] = v.y;
+                    d[4 * i + 2] = v.z;
+                    d[4 * i + 3] = v.w;
+                }
+                build_rows_hi_chained<kQuant>(d, recip, P);
+                transpose16x2(P);
+                store_words<16>(dst + 16, P, count_words > 16u ? count_words - 16u : 0u,
+                                rmax - 15u);
+            }
+        }
+
+        // g. advance
+        if (!has_next) break;
+        cur = nxt;
+        __builtin_amdgcn_s_waitcnt(0);
+        staged_block(stage, block_exists(p.groups[cur.gi], cur.tile, tid), d, tid);
+        __builtin_amdgcn_s_waitcnt(0);  // LDS reads done before it is refilled
+        has_next = cur.t + G < p.total_tiles;
+        if (has_next) {
+            nxt = tile_ctx(p, cur.t + G, s_gfirst);
+            stage_block(p.groups[nxt.gi], nxt.J.in, nxt.tile, stage, &bad, tid);
+        }
+    }
+    if (bad & 1) flag_error(p.error, p.host_ctl, kErrLayerIndex);
 }
 
 // ---- relative-bound pre-pass (jobs too long for the fused exchange) -------
@@ -1072,6 +1490,16 @@ hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
     return hipGetLastError();
 }
 
+hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
+                                     hipStream_t stream, hipEvent_t start,
+                                     hipEvent_t stop) {
+    if (p.quantizer)
+        launch(compress_pipelined_kernel<1>, grid, stream, start, stop, p);
+    else
+        launch(compress_pipelined_kernel<0>, grid, stream, start, stop, p);
+    return hipGetLastError();
+}
+
 hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
                          hipStream_t stream, hipEvent_t start) {
     launch(minmax_kernel, grid, stream, start, nullptr, p);
@@ -1094,11 +1522,13 @@ hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
     return hipGetLastError();
 }
 
-int compress_resident_workgroups(int device) {
+int compress_resident_workgroups(int device, bool pipelined) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(compress_kernel<0>),
-            kThreads, 0) != hipSuccess)
+    const void* fn = pipelined
+        ? reinterpret_cast<const void*>(compress_pipelined_kernel<0>)
+        : reinterpret_cast<const void*>(compress_kernel<0>);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0) !=
+        hipSuccess)
         per_cu = 1;
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess) return per_cu;

@@ -397,3 +397,26 @@ def test_shim_rejects_invalid_arguments(cpp):
     plain = cpp.CuSZpWrapper(cpp.CompressionConfig(), 0)  # MODE_PLAIN default
     assert plain.compress_batch_fixed_bf16(list(pages), bufs, [1e-4] * 2)[0] is False
     assert w.decompress_batch_fixed_bf16([], [], torch.empty(0, device=DEV), n, [])
+
+
+# ---- both encoder schedules --------------------------------------------------
+# Launches whose blocks are all whole, single-layer and 16-byte aligned use
+# the persistent encoder; KVSZP_PERSISTENT=0 (read when a context is
+# created) selects one workgroup per tile.  Both must write the same bytes.
+
+@pytest.mark.parametrize("persistent", ["1", "0"])
+def test_both_encoder_schedules_match_oracle(cpp, oracle, persistent, monkeypatch):
+    monkeypatch.setenv("KVSZP_PERSISTENT", persistent)
+    n = 36864                                   # 4.5 tiles: a partial last tile
+    pages = rand_pages(4, n, seed=21)
+    const = torch.full((n,), -2.75, dtype=torch.bfloat16, device=DEV)  # rate 31
+    pages = torch.cat([pages, const[None]])
+    for relative, eps in ((True, [1e-4, 1e-5, 2e-4, 1e-3, 1e-4]),
+                          (False, [1e-3, 1e-2, 5e-4, 1e-3, 1e-3])):
+        for quantizer in (0, 1):
+            w = make(cpp, relative=relative, quantizer=quantizer)
+            bufs = buffers(cpp, pages.shape[0], n)
+            ok, sizes, bounds = w.compress_batch_fixed_bf16(list(pages), bufs, eps)
+            assert ok
+            assert_streams(oracle, u16(pages), n, eps, relative, bufs, sizes,
+                           bounds, quantizer=quantizer)
