@@ -36,12 +36,27 @@ namespace kvszp {
 
 // Exchange the columns {c : c & J} of x with the columns {c : !(c & J)} of y
 // (the block-swap step of a recursive bit-matrix transpose).  `mask` selects
-// the columns with (c & J) == 0.
+// the columns with (c & J) == 0.  Written as two bit-selects,
+//     x' = (x & mask) | ((y << J) & ~mask),  y' = ((x >> J) & mask) | (y & ~mask),
+// two instructions each (shift + one 3-input bit op); for J = 8 each half is
+// one byte permute.
 template <int J>
 KVSZP_HD void delta_swap(uint32_t& x, uint32_t& y, uint32_t mask) {
-    const uint32_t t = ((x >> J) ^ y) & mask;
-    y ^= t;
-    x ^= t << J;
+#if defined(__HIP_DEVICE_COMPILE__)
+    if (J == 8) {
+        // bytes of (x, y) = (x0 x1 x2 x3, y0 y1 y2 y3), byte 0 lowest:
+        // x' = (x0 y0 x2 y2), y' = (x1 y1 x3 y3)
+        const uint32_t nx = __builtin_amdgcn_perm(y, x, 0x06020400u);
+        const uint32_t ny = __builtin_amdgcn_perm(y, x, 0x07030501u);
+        x = nx;
+        y = ny;
+        return;
+    }
+#endif
+    const uint32_t nx = (x & mask) | ((y << J) & ~mask);
+    const uint32_t ny = ((x >> J) & mask) | (y & ~mask);
+    x = nx;
+    y = ny;
 }
 
 // Transposes rows [0,16) as two independent 16x16 bit matrices (low and high

@@ -1281,13 +1281,13 @@ __device__ __forceinline__ void store_block(uint16_t* dst, const uint32_t* out,
 //
 // The wide path parks the high fields in LDS (`park`, one column per thread)
 // so that only one set of 16 rows is held in registers at a time.
-template <bool kWide>
+template <bool kWide, bool kEb2>
 __device__ __forceinline__ void decode_words(const uint32_t* src,
                                              uint32_t count_words, uint32_t rmax,
-                                             float eb, uint32_t rate,
-                                             uint32_t* out,
+                                             float eb, uint32_t rate, uint32_t* out,
                                              uint32_t (*park)[kThreads]) {
     const int tid = threadIdx.x;
+    const float eb2 = eb * 2.0f;
     if (kWide) {
         uint32_t H[16];
         load_words<16>(src + 16, H, count_words > 16u ? count_words - 16u : 0u,
@@ -1317,13 +1317,22 @@ __device__ __forceinline__ void decode_words(const uint32_t* src,
             m0 |= ((park[k0][tid] >> sh0) & 0xFFFFu) << 15;
             m1 |= ((park[k1][tid] >> sh1) & 0xFFFFu) << 15;
         }
-        const int32_t q0 = (lo0 & 1u) ? -(int32_t)m0 : (int32_t)m0;
-        const int32_t q1 = (lo1 & 1u) ? -(int32_t)m1 : (int32_t)m1;
+        // q = sign ? -m : m as (m ^ -sign) + sign
+        const uint32_t s0 = lo0 & 1u, s1 = lo1 & 1u;
+        const int32_t q0 = (int32_t)((m0 ^ (0u - s0)) + s0);
+        const int32_t q1 = (int32_t)((m1 ^ (0u - s1)) + s1);
         f32x2 y;
-        y.x = ((float)q0 * eb) * 2.0f;
-        y.y = ((float)q1 * eb) * 2.0f;
-        const bf16x2 h = __builtin_convertvector(y, bf16x2);
-        out[i] = rate ? __builtin_bit_cast(uint32_t, h) : 0u;
+        if (kEb2) {
+            // fl(fl(q*eb)*2) == fl(q*(2eb)) while FLT_MIN <= eb <= FLT_MAX/2:
+            // scaling by 2 commutes with rounding for normal results, and
+            // every nonzero |q*eb| >= eb is normal.
+            y.x = (float)q0 * eb2;
+            y.y = (float)q1 * eb2;
+        } else {
+            y.x = ((float)q0 * eb) * 2.0f;
+            y.y = ((float)q1 * eb) * 2.0f;
+        }
+        out[i] = rate ? __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2)) : 0u;
     }
 }
 
@@ -1418,10 +1427,18 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     } else {
         const uint32_t* src = reinterpret_cast<const uint32_t*>(J.in + base);
         const uint32_t count_words = rate ? rate + 1u : 0u;
-        if (rmax <= 15u)
-            decode_words<false>(src, count_words, rmax, J.eb, rate, out, s_park);
-        else
-            decode_words<true>(src, count_words, rmax, J.eb, rate, out, s_park);
+        const bool eb2_ok = J.eb >= FLT_MIN && J.eb <= FLT_MAX / 2;  // uniform
+        if (rmax <= 15u) {
+            if (eb2_ok)
+                decode_words<false, true>(src, count_words, rmax, J.eb, rate, out, s_park);
+            else
+                decode_words<false, false>(src, count_words, rmax, J.eb, rate, out, s_park);
+        } else {
+            if (eb2_ok)
+                decode_words<true, true>(src, count_words, rmax, J.eb, rate, out, s_park);
+            else
+                decode_words<true, false>(src, count_words, rmax, J.eb, rate, out, s_park);
+        }
     }
 
     if (count && (rate != 0 || p.rate0_zero)) {
