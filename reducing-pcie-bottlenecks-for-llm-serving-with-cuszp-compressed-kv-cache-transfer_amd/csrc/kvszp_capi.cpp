@@ -90,6 +90,7 @@ struct kvszp_ctx {
     // Persistent encoder grid (co-resident workgroups); 0 = one workgroup
     // per tile (KVSZP_PERSISTENT=0, or ticket mode).
     uint32_t pipelined_grid = 0;
+    uint32_t decompress_grid = 0;   // persistent decoder grid (0 = off)
     // control words: [0] ticket counter, [1] low 32 bits = error word
     unsigned long long* control = nullptr;
     unsigned long long ticket_next = 0;
@@ -550,8 +551,15 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     g.tiles_per_job = tiles_per_job;
     g.header_bytes = R;
     const int rec = timing_begin(c, KVSZP_KERNEL_DECOMPRESS);
-    hipError_t e = launch_decompress(p, stream, timing_start(c, rec),
-                                     timing_stop(c, rec));
+    hipError_t e;
+    if (c->decompress_grid != 0 && tiles_per_job <= kDirectPrefixTiles + 1) {
+        p.ticket = nullptr;
+        const uint32_t grid = (uint32_t)std::min<uint64_t>(total_tiles, c->decompress_grid);
+        e = launch_decompress_pipelined(p, grid, stream, timing_start(c, rec),
+                                        timing_stop(c, rec));
+    } else {
+        e = launch_decompress(p, stream, timing_start(c, rec), timing_stop(c, rec));
+    }
     if (e != hipSuccess) return hip_fail(e, "decompress launch");
     c->ticket_next += total_tiles;
     return KVSZP_OK;
@@ -606,11 +614,14 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
         const bool off = (env && env[0] == '0') || c->use_tickets;
         c->pipelined_grid =
             off ? 0u : (uint32_t)std::max(0, compress_resident_workgroups(device_id, true));
+        c->decompress_grid =
+            off ? 0u : (uint32_t)std::max(0, decompress_resident_workgroups(device_id));
     }
     if (const char* dbg = std::getenv("KVSZP_DEBUG"); dbg && dbg[0] == '1')
         std::fprintf(stderr, "kvszp: device %d resident encoder workgroups %d, "
-                     "fused tile limit %u, persistent grid %u\n", device_id,
-                     resident, c->fused_tile_limit, c->pipelined_grid);
+                     "fused tile limit %u, persistent grids %u / %u\n", device_id,
+                     resident, c->fused_tile_limit, c->pipelined_grid,
+                     c->decompress_grid);
     *out = c;
     return KVSZP_OK;
 }

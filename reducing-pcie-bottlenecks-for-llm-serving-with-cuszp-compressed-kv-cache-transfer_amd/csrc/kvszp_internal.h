@@ -152,6 +152,12 @@ hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
                          hipStream_t stream, hipEvent_t start);
 hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
                              hipEvent_t start, hipEvent_t stop);
+// Persistent decoder (jobs of at most kDirectPrefixTiles + 1 tiles): `grid`
+// workgroups walk the tiles; it has no cross-workgroup waits.
+hipError_t launch_decompress_pipelined(const DecompressParams& p, uint32_t grid,
+                                       hipStream_t stream, hipEvent_t start,
+                                       hipEvent_t stop);
+int decompress_resident_workgroups(int device);
 // Maximum co-resident workgroups of an encoder kernel on this device.
 int compress_resident_workgroups(int device, bool pipelined);
 

@@ -1281,11 +1281,13 @@ __device__ __forceinline__ void store_block(uint16_t* dst, const uint32_t* out,
 //
 // The wide path parks the high fields in LDS (`park`, one column per thread)
 // so that only one set of 16 rows is held in registers at a time.
-template <bool kWide, bool kEb2>
+// kPre: words w_0..w_15 were loaded by the caller into `pre`.
+template <bool kWide, bool kEb2, bool kPre = false>
 __device__ __forceinline__ void decode_words(const uint32_t* src,
                                              uint32_t count_words, uint32_t rmax,
                                              float eb, uint32_t rate, uint32_t* out,
-                                             uint32_t (*park)[kThreads]) {
+                                             uint32_t (*park)[kThreads],
+                                             const uint32_t* pre = nullptr) {
     const int tid = threadIdx.x;
     const float eb2 = eb * 2.0f;
     if (kWide) {
@@ -1299,8 +1301,13 @@ __device__ __forceinline__ void decode_words(const uint32_t* src,
         __asm__ volatile("" ::: "memory");
     }
     uint32_t L[16];
-    load_words<16>(src, L, count_words < 16u ? count_words : 16u,
-                   rmax < 15u ? rmax + 1u : 16u);
+    if (kPre) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) L[k] = pre[k];
+    } else {
+        load_words<16>(src, L, count_words < 16u ? count_words : 16u,
+                       rmax < 15u ? rmax + 1u : 16u);
+    }
     transpose16x2(L);  // L[k]: low fields of elements k^7, 16+(k^7)
     // out[i] holds elements 2i and 2i+1.  Rows k0, k1 feed both out[j]
     // (low halves) and out[j + 8] (high halves), so they are consumed
@@ -1333,6 +1340,80 @@ __device__ __forceinline__ void decode_words(const uint32_t* src,
             y.y = ((float)q1 * eb) * 2.0f;
         }
         out[i] = rate ? __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2)) : 0u;
+    }
+}
+
+// One block: stream words at `base` -> 16 packed BF16 pairs (zeros when the
+// whole wave has rate 0).
+__device__ __forceinline__ void decode_block(const uint8_t* in, uint64_t base,
+                                             uint32_t rate, uint32_t rmax, float eb,
+                                             uint32_t* out,
+                                             uint32_t (*park)[kThreads]) {
+    if (rmax == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) out[i] = 0;
+        return;
+    }
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(in + base);
+    const uint32_t count_words = rate ? rate + 1u : 0u;
+    const bool eb2_ok = eb >= FLT_MIN && eb <= FLT_MAX / 2;  // uniform
+    if (rmax <= 15u) {
+        if (eb2_ok)
+            decode_words<false, true>(src, count_words, rmax, eb, rate, out, park);
+        else
+            decode_words<false, false>(src, count_words, rmax, eb, rate, out, park);
+    } else {
+        if (eb2_ok)
+            decode_words<true, true>(src, count_words, rmax, eb, rate, out, park);
+        else
+            decode_words<true, false>(src, count_words, rmax, eb, rate, out, park);
+    }
+}
+
+// Writes one decoded block to its destination (cu:539-606): contiguous page,
+// multi-destination split, or layer-indexed position in the full page.
+template <int kDst>
+__device__ __forceinline__ void store_decoded(const DecompressParams& p,
+                                              const Group& g, const DecompressJob& J,
+                                              uint32_t job, uint32_t tile, int tid,
+                                              uint64_t e0, uint32_t count,
+                                              const uint32_t* out, uint32_t& err) {
+    if (kDst == kDstLinear) {
+        store_block(J.dst + e0, out, count, p.aligned16 != 0);
+    } else if (kDst == kDstMulti) {
+        const uint64_t epd = p.elements_per_dest;
+        const uint64_t di = e0 / epd;
+        const uint64_t off = e0 - di * epd;
+        if (off + count <= epd) {
+            uint16_t* dst = p.dests[(uint64_t)job * p.dests_per_page + di] + off;
+            store_block(dst, out, count, ((uintptr_t)dst & 15u) == 0);
+        } else {
+            for (uint32_t v = 0; v < count; ++v) {
+                const uint64_t e = e0 + v;
+                const uint64_t dv = e / epd;
+                uint16_t* dst = p.dests[(uint64_t)job * p.dests_per_page + dv];
+                to_global(dst)[e - dv * epd] = (uint16_t)((v & 1) ? (out[v >> 1] >> 16)
+                                                       : (out[v >> 1] & 0xFFFFu));
+            }
+        }
+    } else {
+        uint32_t badl = 0;
+        const LayerCursor c = layer_cursor(g, (uint64_t)tile * kTileElems,
+                                           (uint32_t)tid * kBlockElems, &badl);
+        if (c.contiguous && !badl) {
+            uint16_t* dst = J.dst + c.src_index;
+            store_block(dst, out, count, ((uintptr_t)dst & 15u) == 0);
+        } else {
+            for (uint32_t v = 0; v < count; ++v) {
+                const uint64_t s = map_index(e0 + v, g.layers, g.selected_layers,
+                                             g.source_layers, g.elements_per_layer,
+                                             &badl);
+                if (badl) break;
+                to_global(J.dst)[s] = (uint16_t)((v & 1) ? (out[v >> 1] >> 16)
+                                              : (out[v >> 1] & 0xFFFFu));
+            }
+        }
+        if (badl) err |= kErrLayerIndex;
     }
 }
 
@@ -1421,65 +1502,99 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     // y = bf16_rne((float(q) * eb) * 2) (cu:535-538).
     const uint32_t rmax = wave_max(rate);
     uint32_t out[16];
-    if (rmax == 0) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) out[i] = 0;
-    } else {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(J.in + base);
-        const uint32_t count_words = rate ? rate + 1u : 0u;
-        const bool eb2_ok = J.eb >= FLT_MIN && J.eb <= FLT_MAX / 2;  // uniform
-        if (rmax <= 15u) {
-            if (eb2_ok)
-                decode_words<false, true>(src, count_words, rmax, J.eb, rate, out, s_park);
-            else
-                decode_words<false, false>(src, count_words, rmax, J.eb, rate, out, s_park);
-        } else {
-            if (eb2_ok)
-                decode_words<true, true>(src, count_words, rmax, J.eb, rate, out, s_park);
-            else
-                decode_words<true, false>(src, count_words, rmax, J.eb, rate, out, s_park);
-        }
-    }
+    decode_block(J.in, base, rate, rmax, J.eb, out, s_park);
+    if (count && (rate != 0 || p.rate0_zero))
+        store_decoded<kDst>(p, g, J, job, tile, tid, e0, count, out, err);
+    if (err) flag_error(p.error, p.host_ctl, err);
+}
 
-    if (count && (rate != 0 || p.rate0_zero)) {
-        if (kDst == kDstLinear) {
-            store_block(J.dst + e0, out, count, p.aligned16 != 0);
-        } else if (kDst == kDstMulti) {
-            const uint64_t epd = p.elements_per_dest;
-            const uint64_t di = e0 / epd;
-            const uint64_t off = e0 - di * epd;
-            if (off + count <= epd) {
-                uint16_t* dst = p.dests[(uint64_t)job * p.dests_per_page + di] + off;
-                store_block(dst, out, count,
-                            ((uintptr_t)dst & 15u) == 0);
-            } else {
-                for (uint32_t v = 0; v < count; ++v) {
-                    const uint64_t e = e0 + v;
-                    const uint64_t dv = e / epd;
-                    uint16_t* dst = p.dests[(uint64_t)job * p.dests_per_page + dv];
-                    to_global(dst)[e - dv * epd] = (uint16_t)((v & 1) ? (out[v >> 1] >> 16)
-                                                           : (out[v >> 1] & 0xFFFFu));
-                }
-            }
-        } else {
-            uint32_t badl = 0;
-            const LayerCursor c = layer_cursor(g, (uint64_t)tile * kTileElems,
-                                               (uint32_t)tid * kBlockElems, &badl);
-            if (c.contiguous && !badl) {
-                uint16_t* dst = J.dst + c.src_index;
-                store_block(dst, out, count, ((uintptr_t)dst & 15u) == 0);
-            } else {
-                for (uint32_t v = 0; v < count; ++v) {
-                    const uint64_t s = map_index(e0 + v, g.layers, g.selected_layers,
-                                                 g.source_layers,
-                                                 g.elements_per_layer, &badl);
-                    if (badl) break;
-                    to_global(J.dst)[s] = (uint16_t)((v & 1) ? (out[v >> 1] >> 16)
-                                                  : (out[v >> 1] & 0xFFFFu));
-                }
-            }
-            if (badl) err |= kErrLayerIndex;
+// Persistent decoder for launches whose jobs have at most
+// kDirectPrefixTiles + 1 tiles (every tile's offset comes from the header,
+// so no workgroup waits for another).  Workgroup w decodes tiles w, w + G,
+// ...; the header words the next tile needs (its own rates and the rate
+// bytes of its job's earlier tiles) are requested before the current tile's
+// payload is decoded, so their latency overlaps the current tile's.  (A
+// deeper pipeline that also prefetches the next payload holds ~90 VGPRs and
+// measured slower at the lower occupancy.)
+template <int kDst>
+__global__ __launch_bounds__(kThreads) void decompress_pipelined_kernel(
+    DecompressParams p) {
+    constexpr int kPreWords = (int)(kDirectPrefixTiles * (kTileBlocks / 4) / kThreads);
+    __shared__ uint32_t s_wave[kThreads / 64];
+    __shared__ uint32_t s_pre[kThreads / 64];
+    __shared__ uint32_t s_hdr[kTileBlocks / 4];
+    __shared__ uint32_t s_park[16][kThreads];  // wide-rate decode scratch
+
+    publish_seq(p.host_ctl, p.seq);
+    const Group& g = p.groups[0];
+    const uint32_t G = gridDim.x;
+    const uint32_t tpj = g.tiles_per_job;
+    const uint64_t n = g.n;
+    const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
+    const uint32_t R = g.header_bytes;
+    uint32_t err = 0;
+
+    // Header words of tile tt: this thread's word of the tile's own rates
+    // (threads < 64) and its share of the earlier tiles' rate words.
+    uint32_t hw = 0, pw[kPreWords];
+    auto request_header = [&](uint32_t tt, int tid) {
+        const uint32_t job = tt / tpj, tile = tt - job * tpj;
+        const uint32_t* words = reinterpret_cast<const uint32_t*>(load_const(p.jobs, job).in);
+        hw = tid < kTileBlocks / 4 ? to_global(words)[tile * (kTileBlocks / 4) + tid] : 0u;
+#pragma unroll
+        for (int i = 0; i < kPreWords; ++i) {
+            const uint32_t k = (uint32_t)(tid + i * kThreads);
+            pw[i] = k < tile * (kTileBlocks / 4) ? to_global(words)[k] : 0u;
         }
+    };
+
+    uint32_t t = blockIdx.x;
+    request_header(t, (int)threadIdx.x);
+    for (;;) {
+        const int tid = loop_tid();
+        const int lane = tid & 63;
+        const int wave = tid >> 6;
+        const uint32_t job = t / tpj, tile = t - job * tpj;
+        const DecompressJob J = load_const(p.jobs, job);
+        const uint32_t b = tile * kTileBlocks + tid;
+        const uint64_t e0 = (uint64_t)b * kBlockElems;
+        const uint32_t count =
+            b < nb ? (uint32_t)(n - e0 < kBlockElems ? n - e0 : kBlockElems) : 0u;
+
+        // Rates (cu:410-418; padding bytes masked) and the earlier tiles'
+        // payload bytes from the words requested last iteration.
+        if (tid < kTileBlocks / 4) s_hdr[tid] = hw;
+        __syncthreads();
+        uint32_t part = 0;
+#pragma unroll
+        for (int i = 0; i < kPreWords; ++i) part += header_word_bytes(pw[i]);
+        part = wave_sum(part);
+        if (lane == 0) s_pre[wave] = part;
+        uint32_t rate = count ? (s_hdr[tid >> 2] >> (8 * (tid & 3))) & 0xFFu : 0u;
+        if (rate > 31u) {
+            err |= kErrRate;
+            rate = 0;
+        }
+        const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
+        const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
+        const uint32_t prefix = s_pre[0] + s_pre[1] + s_pre[2] + s_pre[3];
+        const uint64_t base = (uint64_t)R + prefix + sc.exclusive;
+        if (rate && base + bytes > J.size) {
+            err |= kErrTruncated;
+            rate = 0;
+        }
+
+        // Ask for the next tile's header words, then decode this tile.
+        const bool has_next = t + G < p.total_tiles;
+        if (has_next) request_header(t + G, tid);
+
+        const uint32_t rmax = wave_max(rate);
+        uint32_t out[16];
+        decode_block(J.in, base, rate, rmax, J.eb, out, s_park);
+        if (count && (rate != 0 || p.rate0_zero))
+            store_decoded<kDst>(p, g, J, job, tile, tid, e0, count, out, err);
+        if (!has_next) break;
+        t += G;
     }
     if (err) flag_error(p.error, p.host_ctl, err);
 }
@@ -1521,6 +1636,34 @@ hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
                          hipStream_t stream, hipEvent_t start) {
     launch(minmax_kernel, grid, stream, start, nullptr, p);
     return hipGetLastError();
+}
+
+hipError_t launch_decompress_pipelined(const DecompressParams& p, uint32_t grid,
+                                       hipStream_t stream, hipEvent_t start,
+                                       hipEvent_t stop) {
+    switch (p.dst_kind) {
+    case kDstMulti:
+        launch(decompress_pipelined_kernel<kDstMulti>, grid, stream, start, stop, p);
+        break;
+    case kDstIndexed:
+        launch(decompress_pipelined_kernel<kDstIndexed>, grid, stream, start, stop, p);
+        break;
+    default:
+        launch(decompress_pipelined_kernel<kDstLinear>, grid, stream, start, stop, p);
+        break;
+    }
+    return hipGetLastError();
+}
+
+int decompress_resident_workgroups(int device) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(decompress_pipelined_kernel<kDstIndexed>),
+            kThreads, 0) != hipSuccess)
+        per_cu = 1;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return per_cu;
+    return per_cu * prop.multiProcessorCount;
 }
 
 hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,

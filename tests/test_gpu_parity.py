@@ -420,3 +420,25 @@ def test_both_encoder_schedules_match_oracle(cpp, oracle, persistent, monkeypatc
             assert ok
             assert_streams(oracle, u16(pages), n, eps, relative, bufs, sizes,
                            bounds, quantizer=quantizer)
+
+
+@pytest.mark.parametrize("persistent", ["1", "0"])
+@pytest.mark.parametrize("rate0", [0, 1])
+def test_both_decoder_schedules_match_oracle(cpp, oracle, persistent, rate0,
+                                            monkeypatch):
+    monkeypatch.setenv("KVSZP_PERSISTENT", persistent)
+    n = 36864 + 40                              # partial last block and tile
+    pages = rand_pages(5, n, seed=31)
+    pages[2, :9000] = 0                         # rate-0 blocks
+    pages[3] = torch.full((n,), 7.0, dtype=torch.bfloat16, device=DEV)
+    w = make(cpp, rate0=rate0)
+    bufs, sizes, bounds = _encode(cpp, w, pages, [1e-4, 1e-5, 1e-4, 1e-4, 1e-3])
+    pre = u16(torch.full((n,), 1.75, dtype=torch.bfloat16))
+    out = torch.full((5 * n,), 1.75, dtype=torch.bfloat16, device=DEV)
+    assert w.decompress_batch_fixed_bf16(bufs, sizes, out, n, bounds)
+    assert w.synchronize()
+    got = u16(out)
+    for i in range(5):
+        want = oracle.decompress_contiguous(bufs[i][:sizes[i]].cpu().numpy(), n,
+                                            bounds[i], rate0, pre.copy())
+        assert np.array_equal(got[i * n:(i + 1) * n], want), f"page {i}"
