@@ -218,10 +218,10 @@ def _pmc_per_dispatch(run_dir: str, counter: str) -> dict:
     out = defaultdict(list)
     for did in sorted(per):
         name = names[did]
-        if "compress_kernel" in name and "decompress" not in name:
-            kind = "compress_kernel"
-        elif "decompress_kernel" in name:
-            kind = "decompress_kernel"
+        if "kvszp::" in name and "decompress" in name:
+            kind = "decompress_kernel"   # decompress_kernel / decompress_pipelined_kernel
+        elif "kvszp::" in name and "compress" in name and "minmax" not in name:
+            kind = "compress_kernel"     # compress_kernel / compress_pipelined_kernel
         elif "copyBuffer" in name:
             kind = "copy"
         else:
