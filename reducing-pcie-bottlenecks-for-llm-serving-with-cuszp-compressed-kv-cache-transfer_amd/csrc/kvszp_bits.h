@@ -83,6 +83,28 @@ KVSZP_HD int row_hi_elem(int k) { return 16 + (k ^ 7); }
 KVSZP_HD uint32_t field_lo(uint32_t m, uint32_t s) { return ((m << 1) | s) & 0xFFFFu; }
 KVSZP_HD uint32_t field_hi(uint32_t m) { return (m >> 15) & 0xFFFFu; }
 
+// The whole field 2|q| + sign of the reference quantizer's q
+// (cuszp_batched_fixed.cu:10-25: v = fl(x*r), s = !(v >= -0.5),
+// t = fl(v + 0.5) or fl(x*r + 0.5), q = cvt.rzi(t) - s) from t alone, for
+// |t| < 2^31 (the conversion does not saturate):
+//   * the sign test on v equals a test on t.  Two roundings: v >= -0.5 iff
+//     t >= 0 (for v in [-1, -0.5) the sum v + 0.5 is exact by Sterbenz, below
+//     that t <= -0.5).  Fused: v >= -0.5 iff the exact product p is at least
+//     -0.5 - 2^-25 (the rounding midpoint below -0.5, ties to -0.5), iff
+//     t >= -2^-25: near -0.5, p (an 8-bit by 24-bit significand product) is
+//     a multiple of 2^-33, so no p + 0.5 lies in the half-ulp interval
+//     [-2^-25 - 2^-49, -2^-25) where the two tests could disagree.  NaN
+//     fails both tests (s = 1).
+//   * with c = trunc(|t|) (NaN -> 0): s = 0 gives q = c; s = 1 means t < 0
+//     or NaN, q = -c - 1.  So |q| = c + s and the field is 2(c + s) + s.
+constexpr float kFusedSignThreshold = 0x1p-25f;
+KVSZP_HD bool field_sign(float t, int fused) {
+    return fused ? !(t >= -kFusedSignThreshold) : !(t >= 0.0f);
+}
+KVSZP_HD uint32_t field_from_trunc(uint32_t c, bool s) {
+    return (c << 1) + (s ? 3u : 0u);  // = 2(c + s) + s
+}
+
 // Reference-free host helpers (used by the host test): a[v] = |q_v| with the
 // sign in bit 31, element order.  words[0..31] receive w_0..w_31.
 KVSZP_HD void pack_block_words(const uint32_t* a, uint32_t* words) {

@@ -175,6 +175,22 @@ __device__ __forceinline__ int32_t quantize(float x, float recip) {
     return (int32_t)((uint32_t)cvt_rzi_sat(t) - s);
 }
 
+// trunc(|t|) as an unsigned integer, NaN -> 0 (v_cvt_u32_f32 with the abs
+// modifier; the callers keep |t| below 2^31).
+__device__ __forceinline__ uint32_t cvt_abs_u32(float t) {
+    uint32_t c;
+    asm("v_cvt_u32_f32 %0, |%1|" : "=v"(c) : "v"(t));
+    return c;
+}
+
+// Field 2|q| + sign of quantize<kQuant>(x, recip), for |t| < 2^31
+// (field_sign / field_from_trunc state the identity).
+template <int kQuant>
+__device__ __forceinline__ uint32_t quant_field(float x, float recip) {
+    const float t = kQuant ? __builtin_fmaf(x, recip, 0.5f) : x * recip + 0.5f;
+    return field_from_trunc(cvt_abs_u32(t), field_sign(t, kQuant));
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t d) {
     return __uint_as_float(d << 16);
 }
@@ -628,6 +644,28 @@ __device__ __forceinline__ void build_rows_lo_chained(const uint32_t* d, float r
     }
 }
 
+// Rows of low fields for a full block whose |t| all stay below 2^31, and
+// the OR of the whole fields (its value >> 1 is the OR of all |q|).  Rows
+// are chained through the block's data words rather than the reciprocal
+// (no register copy per row).
+template <int kQuant>
+__device__ __forceinline__ void build_rows_fast_chained(uint32_t* d, float recip,
+                                                        uint32_t* P, uint32_t& orf) {
+    uint32_t prev = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int e0 = row_lo_elem(k), e1 = row_hi_elem(k);
+        asm volatile("" : "+v"(d[e0 >> 1]), "+v"(d[e1 >> 1]) : "v"(prev));
+        const float x0 = (e0 & 1) ? bf16_hi(d[e0 >> 1]) : bf16_lo(d[e0 >> 1]);
+        const float x1 = (e1 & 1) ? bf16_hi(d[e1 >> 1]) : bf16_lo(d[e1 >> 1]);
+        const uint32_t f0 = quant_field<kQuant>(x0, recip);
+        const uint32_t f1 = quant_field<kQuant>(x1, recip);
+        orf |= f0 | f1;
+        P[k] = __builtin_amdgcn_perm(f1, f0, 0x05040100u);  // low halves
+        prev = P[k];
+    }
+}
+
 template <int kQuant>
 __device__ __forceinline__ void build_rows_hi_chained(const uint32_t* d, float recip,
                                                       uint32_t* P) {
@@ -903,6 +941,23 @@ __device__ __forceinline__ uint64_t block_source(const Group& g, uint32_t tile,
     const uint64_t tile_first = (uint64_t)tile * kTileElems;
     const uint32_t elem = (uint32_t)tid * kBlockElems;
     if (g.layers == nullptr) return tile_first + elem;
+    // A tile inside one layer reads the layer map once, as a scalar load: a
+    // vector load would also wait for the stores this wave just issued.
+    const uint64_t per_prefix = g.selected_layers * g.elements_per_layer;
+    const uint64_t t_prefix = tile_first / per_prefix;
+    const uint32_t t_within = (uint32_t)(tile_first - t_prefix * per_prefix);
+    const uint32_t epl = (uint32_t)g.elements_per_layer;
+    const uint32_t layer = t_within / epl;
+    const uint32_t inner = t_within - layer * epl;
+    if (inner + (uint32_t)kTileElems <= epl) {
+        int64_t l = load_const(g.layers, layer);
+        if (l < 0 || (uint64_t)l >= g.source_layers) {
+            *bad = 1;
+            l = 0;
+        }
+        return (t_prefix * g.source_layers + (uint64_t)l) * g.elements_per_layer +
+               inner + elem;
+    }
     return layer_cursor(g, tile_first, elem, bad).src_index;
 }
 
@@ -1096,18 +1151,28 @@ __attribute__((amdgpu_waves_per_eu(6, 6))) void compress_pipelined_kernel(
 
         // a. bound
         float eb = cur.J.eps;
+        float M = FLT_MAX;  // bound on every |x| of the job
         if (fused) {
             uint32_t kmin, kmax;
             exchange_minmax(p, cur.t - cur.tile, g.tiles_per_job, s_xmin, s_xmax,
                             kmin, kmax, tid);
             eb = relative_bound(cur.J.eps, kmin, kmax);
+            M = fmaxf(fabsf(min_key_value(kmin)), fabsf(max_key_value(kmax)));
         }
         const float recip = 0.5f / eb;  // cu:166, IEEE division
+        // Whole fields straight from t when no |t| can reach 2^31.
+        const bool fast = fused && M * recip < 0x1p30f;
 
         // b. quantize (cu:180-231); a block past the end has d = 0 -> rate 0
         uint32_t P[16];
         uint32_t orv = 0;
-        build_rows_lo_chained<kQuant>(d, recip, P, orv);
+        if (fast) {
+            uint32_t orf = 0;
+            build_rows_fast_chained<kQuant>(d, recip, P, orf);
+            orv = orf >> 1;
+        } else {
+            build_rows_lo_chained<kQuant>(d, recip, P, orv);
+        }
         const uint32_t rate = (ex && orv) ? 32u - (uint32_t)__builtin_clz(orv) : 0u;
         const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
         s_rate[tid] = (uint8_t)rate;
@@ -1478,7 +1543,9 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
     uint32_t prefix;
     if (direct) {
-        prefix = s_pre[0] + s_pre[1] + s_pre[2] + s_pre[3];
+        prefix = 0;
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) prefix += s_pre[w];
         if (tid == 0 && g.tiles_per_job > kDirectPrefixTiles + 1)
             store_relaxed(&p.tile_state[t],
                           ((unsigned long long)(p.epoch * 4u + 2u) << 32) |
@@ -1577,7 +1644,9 @@ __global__ __launch_bounds__(kThreads) void decompress_pipelined_kernel(
         }
         const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
         const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
-        const uint32_t prefix = s_pre[0] + s_pre[1] + s_pre[2] + s_pre[3];
+        uint32_t prefix = 0;
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) prefix += s_pre[w];
         const uint64_t base = (uint64_t)R + prefix + sc.exclusive;
         if (rate && base + bytes > J.size) {
             err |= kErrTruncated;
