@@ -1,0 +1,296 @@
+"""The benchmark configurations other than the measured one, at full size,
+through the drop-in API (``cuszp_wrapper_cpp``).
+
+Config 1 (the bench workload) is checked by ``bench.py``'s round trip and by
+``test_pipeline_gpu.py``.  Here:
+
+* config 0: one Qwen2.5-1.5B layer, K and V as two pages of 1 048 576
+  values, REL 1e-4, contiguous restore -- small enough for the oracle to
+  check every byte and every decoded value;
+* config 2: 16 requests x 8192 tokens in a shared page pool (8192 pages of
+  229 376 values), compressed in a seeded page-table order and restored into
+  freshly permuted slots;
+* config 3: Qwen2.5-7B, 32K tokens (2048 pages of 458 752 values, RoPE-like
+  K, REL 1e-5);
+* config 4: Llama-3-8B, 64K tokens (4096 pages of 1 048 576 values, 2^32
+  values in all; zero, constant, heavy-tailed and Gaussian pages), per-layer
+  bounds alternating 1e-4 / 1e-5 through the grouped indexed calls: 8192
+  segments, 2^27 blocks in one launch.
+
+At these sizes the oracle checks a sample of pages byte for byte.  Every page
+is checked through size-independent properties, on the GPU:
+  - the returned bound equals fl(eps * max(fl(max - min), 1e-6)) of the page;
+  - the header holds each block's rate, computed from q = quantize(x)
+    (cuszp_batched_fixed.cu:10-31, restated below in torch and itself
+    checked against the oracle on the sampled pages), and zero padding;
+  - the stream size is S = R + sum over blocks of (4 + 4r) for r > 0;
+  - every restored value equals bf16_rne(fl(fl(q * eb) * 2)) bit for bit
+    (cu:535-538), so the restore also lands in the right slots;
+  - where |q| <= 2^24 (so (float)q is exact), |x - x_hat| <= 2 eb (the
+    reference's BF16 tolerance, tests/test_vllm_v1_compressed_offload.py:457)
+    plus the fp32 rounding slack eb * |q| * 2^-22.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+BLOCK = 32
+TILE = 32768  # reference tile: tblock_size(32) * thread_chunk(1024)
+
+
+def make(cpp, eb=1e-4):
+    cfg = cpp.CompressionConfig(eb, True, cpp.DIM_1D, cpp.MODE_FIXED,
+                                cpp.TYPE_FLOAT)
+    return cpp.CuSZpWrapper(cfg, 0)
+
+
+def header_bytes(n: int) -> int:
+    return 1024 * ((n + TILE - 1) // TILE)
+
+
+def stream_slab(batch: int, n: int):
+    """One slab, `batch` caller buffers of the API's 8N-byte capacity."""
+    cap = 8 * n
+    slab = torch.empty(batch, cap, dtype=torch.uint8, device=DEV)
+    return slab, list(slab)
+
+
+def u16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def relative_bounds(x: torch.Tensor, eps) -> np.ndarray:
+    """cu:55-133 per row: fl(eps * max(fl(max - min), 1e-6f))."""
+    mx = x.float().amax(dim=1).cpu().numpy().astype(np.float32)
+    mn = x.float().amin(dim=1).cpu().numpy().astype(np.float32)
+    rng = np.maximum(mx - mn, np.float32(1e-6))
+    return (np.asarray(eps, dtype=np.float32) * rng).astype(np.float32)
+
+
+def quantize_t(x: torch.Tensor, recip: torch.Tensor) -> torch.Tensor:
+    """cu:10-25, two roundings, per row: int64 q in the int32 range."""
+    v = x.float() * recip[:, None]                  # fl(x * recip)
+    s = (~(v >= -0.5)).to(torch.int64)              # NaN -> 1
+    t = (v + 0.5).double()                          # fl(v + 0.5), exact in f64
+    c = torch.where(torch.isnan(t), torch.zeros_like(t),
+                    t.trunc().clamp(-2.0 ** 31, 2.0 ** 31 - 1)).to(torch.int64)
+    q = c - s
+    return torch.where(q < -2 ** 31, q + 2 ** 32, q)  # int32 wrap
+
+
+def dequant_t(q: torch.Tensor, eb: torch.Tensor) -> torch.Tensor:
+    """cu:535-538: bf16_rne(fl(fl((float)q * eb) * 2))."""
+    return ((q.to(torch.int32).float() * eb[:, None]) * 2.0).to(torch.bfloat16)
+
+
+def block_rates(q: torch.Tensor) -> torch.Tensor:
+    """cu:27-31 per 32-value block: 32 - clz(max |q|) (n % 32 == 0 here)."""
+    m = q.abs().view(q.shape[0], -1, BLOCK).amax(dim=2)
+    r = torch.zeros_like(m)
+    for k in range(32):
+        r += (m >= (1 << k)).to(r.dtype)
+    return r
+
+
+def check_full(x_rows, eb, headers, sizes, restored_rows, n, saturated_ok=False):
+    """Size-independent checks over every page of a chunk.  x_rows /
+    restored_rows: [P, n] bf16 on the GPU (the logical values, in stream
+    order); eb: float32 numpy [P]; headers: [P, R] uint8; sizes: [P]."""
+    ebt = torch.from_numpy(np.asarray(eb, dtype=np.float32)).to(DEV)
+    recip = torch.from_numpy(
+        (np.float32(0.5) / np.asarray(eb, dtype=np.float32)).astype(np.float32)).to(DEV)
+    q = quantize_t(x_rows, recip)
+    rates = block_rates(q)
+    nb = n // BLOCK
+    R = header_bytes(n)
+    assert torch.equal(headers[:, :nb].to(torch.int64), rates), "header rates"
+    assert int(headers[:, nb:R].to(torch.int64).abs().sum()) == 0, "header padding"
+    want_sizes = R + torch.where(rates > 0, 4 + 4 * rates, torch.zeros_like(rates)).sum(1)
+    assert torch.equal(torch.as_tensor(list(sizes), device=DEV, dtype=torch.int64),
+                       want_sizes), "stream sizes"
+    y = dequant_t(q, ebt)
+    same = (y.view(torch.int16) == restored_rows.view(torch.int16))
+    assert bool(same.all()), f"{int((~same).sum())} restored values differ"
+    # The bound holds while (float)q is exact (|q| <= 2^24); fp32 rounding of
+    # x * recip and q * eb adds at most eb * |q| * 2^-22.
+    qmax = q.abs().amax(dim=1)
+    exact = qmax <= 2 ** 24
+    err = (restored_rows.float() - x_rows.float()).abs().amax(dim=1)
+    lim = 2 * ebt + ebt * qmax.float() * 2.0 ** -22
+    assert bool(((err <= lim) | ~exact).all()), "error bound"
+    if not saturated_ok:
+        assert bool(exact.all())
+    return rates
+
+
+def check_sample(oracle, page_bits, n, eps, eb, stream, restored_bits,
+                 layers=None, src=0, epl=0):
+    """Byte and value parity of one page against the oracle."""
+    want_eb = oracle.relative_bound(page_bits, n, eps, layers, src, epl)
+    assert np.float32(eb) == np.float32(want_eb)
+    want = oracle.compress_page(page_bits, n, float(want_eb), layers, src, epl)
+    assert np.array_equal(stream, want)
+    dec = oracle.decompress_contiguous(want, n, float(want_eb))
+    assert np.array_equal(restored_bits, dec)
+
+
+def test_config0_single_layer_round_trip(oracle):
+    """K and V of one Qwen2.5-1.5B layer: every byte and value against the oracle."""
+    import cuszp_wrapper_cpp as cpp
+    import kv_synth
+
+    shape = kv_synth.QWEN25_1P5B_4K
+    k, v = kv_synth.layer_kv(shape, layer=0, seed=0, device=DEV)
+    pages = torch.stack([k.reshape(-1), v.reshape(-1)])
+    n = pages.shape[1]
+    assert n == 1048576
+    w = make(cpp)
+    slab, bufs = stream_slab(2, n)
+    ok, sizes, bounds = w.compress_batch_fixed_bf16(list(pages), bufs, [1e-4, 1e-4])
+    assert ok
+    out = torch.full((2, n), -3.0, dtype=torch.bfloat16, device=DEV)
+    assert w.decompress_batch_fixed_bf16(bufs, sizes, out, n, bounds)
+    assert w.synchronize()
+    bits, got = u16(pages), u16(out)
+    for i in range(2):
+        check_sample(oracle, bits[i], n, 1e-4, bounds[i],
+                     bufs[i][:sizes[i]].cpu().numpy(), got[i])
+    check_full(pages, np.asarray(bounds, np.float32), slab[:, :header_bytes(n)],
+               sizes, out, n)
+
+
+def test_config2_scattered_pool_round_trip(oracle):
+    """16 x 8192-token requests in a shared pool: gather by page table,
+    restore into fresh random slots (single-destination scatter)."""
+    import cuszp_wrapper_cpp as cpp
+    import kv_synth
+
+    shape = kv_synth.QWEN25_1P5B_4K
+    pool = kv_synth.paged_kv(shape, seed=2, device=DEV, tokens=16 * 8192)
+    P, n = pool.shape
+    assert (P, n) == (8192, 229376)
+    g = torch.Generator().manual_seed(2)
+    table = torch.randperm(P, generator=g).tolist()
+    slots = torch.randperm(P, generator=g).tolist()
+    w = make(cpp)
+    slab, bufs = stream_slab(P, n)
+    ok, sizes, bounds = w.compress_batch_fixed_bf16([pool[i] for i in table], bufs,
+                                                    [1e-4] * P)
+    assert ok
+    fresh = torch.full_like(pool, -3.0)
+    assert w.decompress_batch_fixed_bf16_scatter(
+        bufs, sizes, [fresh[s] for s in slots], n, 1, n, bounds)
+    assert w.synchronize()
+    eb = np.asarray(bounds, np.float32)
+    tbl = torch.tensor(table, device=DEV)
+    slt = torch.tensor(slots, device=DEV)
+    assert np.array_equal(eb, relative_bounds(pool[tbl], [1e-4] * P))
+    step = 1024
+    for a in range(0, P, step):
+        check_full(pool[tbl[a:a + step]], eb[a:a + step],
+                   slab[a:a + step, :header_bytes(n)], sizes[a:a + step],
+                   fresh[slt[a:a + step]], n)
+    for i in (0, 1, P // 2, P - 1):
+        check_sample(oracle, u16(pool[table[i]]), n, 1e-4, bounds[i],
+                     bufs[i][:sizes[i]].cpu().numpy(), u16(fresh[slots[i]]))
+
+
+def test_config3_long_context_gqa(oracle):
+    """Qwen2.5-7B shape, 32K tokens, RoPE-like K, REL 1e-5."""
+    import cuszp_wrapper_cpp as cpp
+    import kv_synth
+
+    shape = kv_synth.QWEN25_7B_32K
+    pages = kv_synth.rope_kv(shape, seed=3, device=DEV)
+    P, n = pages.shape
+    assert (P, n) == (2048, 458752)
+    w = make(cpp, 1e-5)
+    slab, bufs = stream_slab(P, n)
+    ok, sizes, bounds = w.compress_batch_fixed_bf16(list(pages), bufs, [1e-5] * P)
+    assert ok
+    g = torch.Generator().manual_seed(3)
+    slots = torch.randperm(P, generator=g).tolist()
+    fresh = torch.full_like(pages, -3.0)
+    assert w.decompress_batch_fixed_bf16_scatter(
+        bufs, sizes, [fresh[s] for s in slots], n, 1, n, bounds)
+    assert w.synchronize()
+    eb = np.asarray(bounds, np.float32)
+    assert np.array_equal(eb, relative_bounds(pages, [1e-5] * P))
+    slt = torch.tensor(slots, device=DEV)
+    step = 256
+    for a in range(0, P, step):
+        check_full(pages[a:a + step], eb[a:a + step],
+                   slab[a:a + step, :header_bytes(n)], sizes[a:a + step],
+                   fresh[slt[a:a + step]], n)
+    for i in (0, 777, P - 1):
+        check_sample(oracle, u16(pages[i]), n, 1e-5, bounds[i],
+                     bufs[i][:sizes[i]].cpu().numpy(), u16(fresh[slots[i]]))
+
+
+def test_config4_stress_pages_indexed_groups(oracle):
+    """Llama-3-8B shape, 64K tokens, 2^32 values: zero, constant,
+    heavy-tailed and Gaussian pages; per-layer bounds alternating
+    1e-4 / 1e-5 through one grouped indexed compress (8192 segments)."""
+    import cuszp_wrapper_cpp as cpp
+    import kv_synth
+
+    shape = kv_synth.LLAMA3_8B_64K
+    pages, classes = kv_synth.stress_pages(shape, seed=4, device=DEV)
+    P = pages.shape[0]
+    assert (P, pages.shape[1]) == (4096, 1048576)
+    epl = shape.elements_per_layer
+    groups = kv_synth.alternating_bound_groups(shape.layers)
+    n = 2 * len(groups[0][1]) * epl
+    assert n == 524288 and all(2 * len(ls) * epl == n for _, ls in groups)
+    idx = [torch.tensor(ls, dtype=torch.long, device=DEV) for _, ls in groups]
+    inputs, eps = [], []
+    for bound, _ in groups:
+        inputs.extend(list(pages))
+        eps.extend([bound] * P)
+    w = make(cpp)
+    slab, bufs = stream_slab(len(groups) * P, n)
+    ok, sizes, bounds = w.compress_batch_fixed_bf16_indexed_groups(
+        inputs, bufs, idx, [P] * len(groups), 2, shape.layers, epl, eps)
+    assert ok
+    dest = torch.full_like(pages, -3.0)
+    for gi in range(len(groups)):
+        lo, hi = gi * P, (gi + 1) * P
+        assert w.decompress_batch_fixed_bf16_indexed_scatter(
+            bufs[lo:hi], sizes[lo:hi], list(dest), idx[gi], 2, shape.layers, epl,
+            bounds[lo:hi])
+    assert w.synchronize()
+    eb = np.asarray(bounds, np.float32)
+    R = header_bytes(n)
+    cls = np.asarray(classes)
+    step = 256
+    for gi, (bound, layers) in enumerate(groups):
+        lsel = torch.tensor(layers, device=DEV)
+        for a in range(0, P, step):
+            b = min(a + step, P)
+            # the segment's logical values: view(2, L, E)[:, layers] flattened
+            seg = pages[a:b].view(b - a, 2, shape.layers, epl)[:, :, lsel].reshape(b - a, n)
+            got = dest[a:b].view(b - a, 2, shape.layers, epl)[:, :, lsel].reshape(b - a, n)
+            k0 = gi * P + a
+            assert np.array_equal(eb[k0:k0 + b - a], relative_bounds(seg, [bound] * (b - a)))
+            rates = check_full(seg, eb[k0:k0 + b - a], slab[k0:k0 + b - a, :R],
+                               sizes[k0:k0 + b - a], got, n, saturated_ok=True)
+            zero = torch.from_numpy(cls[a:b] == "zero").to(DEV)
+            assert int(rates[zero].sum()) == 0  # all-zero pages: S = R
+    # byte parity on a sample of every page class, both groups
+    bits = None
+    for c in ("zero", "constant", "heavy", "gaussian"):
+        p = int(np.nonzero(cls == c)[0][0])
+        bits = u16(pages[p])
+        for gi, (bound, layers) in enumerate(groups):
+            k = gi * P + p
+            want_eb = oracle.relative_bound(bits, n, bound, list(layers), shape.layers, epl)
+            assert np.float32(bounds[k]) == np.float32(want_eb)
+            want = oracle.compress_page(bits, n, float(want_eb), list(layers),
+                                        shape.layers, epl)
+            assert np.array_equal(bufs[k][:sizes[k]].cpu().numpy(), want), (c, gi)
