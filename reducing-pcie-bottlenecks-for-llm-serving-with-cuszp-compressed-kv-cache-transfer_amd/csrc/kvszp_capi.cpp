@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -169,6 +170,23 @@ int ensure_host_results(kvszp_ctx* c, size_t bytes) {
 
 uint32_t host_seq(const kvszp_ctx* c) {
     return __atomic_load_n(&c->host_ctl[kHostSeq], __ATOMIC_ACQUIRE);
+}
+
+// Waits for `stream` to drain.  Polls first (a compress launch lasts tens of
+// microseconds, and a blocking wait adds the wake-up latency of the waiting
+// thread to every call), then blocks if the stream is still busy after
+// kSpinWaitMicros.
+constexpr int64_t kSpinWaitMicros = 2000;
+
+hipError_t wait_stream(hipStream_t stream) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (;;) {
+        const hipError_t e = hipStreamQuery(stream);
+        if (e != hipErrorNotReady) return e;
+        const auto us = std::chrono::duration_cast<std::chrono::microseconds>(
+            std::chrono::steady_clock::now() - t0).count();
+        if (us > kSpinWaitMicros) return hipStreamSynchronize(stream);
+    }
 }
 
 // Copies `bytes` of host data to c->tables through a pinned staging slot;
@@ -461,8 +479,8 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
 
     // The encoder wrote sizes and bounds into pinned host memory; wait for it,
     // since callers need the sizes on the host (cuszp_wrapper.cpp:520-532).
-    e = hipStreamSynchronize(stream);
-    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    e = wait_stream(stream);
+    if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
     rc = consume_device_error(c, stream);
     if (rc) return rc;
     for (size_t i = 0; i < batch; ++i) {
