@@ -52,6 +52,16 @@ KVSZP_HD void delta_swap(uint32_t& x, uint32_t& y, uint32_t mask) {
         y = ny;
         return;
     }
+    // Each output is one shift and one 3-input bit select (v_bitop3_b32,
+    // truth table 0xE4 = S2 ? S0 : S1), written out so the compiler keeps
+    // it at two instructions instead of splitting the masks into ANDs.
+    {
+        const uint32_t nx = __builtin_amdgcn_bitop3_b32(x, y << J, mask, 0xE4);
+        const uint32_t ny = __builtin_amdgcn_bitop3_b32(x >> J, y, mask, 0xE4);
+        x = nx;
+        y = ny;
+        return;
+    }
 #endif
     const uint32_t nx = (x & mask) | ((y << J) & ~mask);
     const uint32_t ny = ((x >> J) & mask) | (y & ~mask);

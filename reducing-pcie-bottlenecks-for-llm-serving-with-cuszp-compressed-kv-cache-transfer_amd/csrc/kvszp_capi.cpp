@@ -570,11 +570,11 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     g.header_bytes = R;
     const int rec = timing_begin(c, KVSZP_KERNEL_DECOMPRESS);
     hipError_t e;
-    if (c->decompress_grid != 0 && tiles_per_job <= kDirectPrefixTiles + 1) {
+    if (c->decompress_grid != 0) {
         p.ticket = nullptr;
         const uint32_t grid = (uint32_t)std::min<uint64_t>(total_tiles, c->decompress_grid);
-        e = launch_decompress_pipelined(p, grid, stream, timing_start(c, rec),
-                                        timing_stop(c, rec));
+        e = launch_decompress_persistent(p, grid, stream, timing_start(c, rec),
+                                         timing_stop(c, rec));
     } else {
         e = launch_decompress(p, stream, timing_start(c, rec), timing_stop(c, rec));
     }

@@ -24,9 +24,6 @@ constexpr int kThreads = kTileBlocks;               // one thread per block
 constexpr int kTileElems = kTileBlocks * kBlockElems;
 constexpr int kRefTileElems = 32768;                // header granularity
 constexpr int kMaxGroups = 16;
-// Decoder: tiles up to this index within a job sum earlier header bytes
-// directly instead of waiting in the look-back.
-constexpr uint32_t kDirectPrefixTiles = 32;
 constexpr uint32_t kSpinLimit = 1u << 20;           // bounded waits (~1 s)
 
 // Device-side error bits (OR-ed into the context's error word).
@@ -152,9 +149,9 @@ hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
                          hipStream_t stream, hipEvent_t start);
 hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
                              hipEvent_t start, hipEvent_t stop);
-// Persistent decoder (jobs of at most kDirectPrefixTiles + 1 tiles): `grid`
-// workgroups walk the tiles; it has no cross-workgroup waits.
-hipError_t launch_decompress_pipelined(const DecompressParams& p, uint32_t grid,
+// Persistent decoder: `grid` workgroups each decode a run of consecutive
+// tiles; it has no cross-workgroup waits.
+hipError_t launch_decompress_persistent(const DecompressParams& p, uint32_t grid,
                                        hipStream_t stream, hipEvent_t start,
                                        hipEvent_t stop);
 int decompress_resident_workgroups(int device);

@@ -1346,15 +1346,52 @@ __device__ __forceinline__ void store_block(uint16_t* dst, const uint32_t* out,
 //
 // The wide path parks the high fields in LDS (`park`, one column per thread)
 // so that only one set of 16 rows is held in registers at a time.
-// kPre: words w_0..w_15 were loaded by the caller into `pre`.
-template <bool kWide, bool kEb2, bool kPre = false>
+template <bool kWide, bool kEb2>
 __device__ __forceinline__ void decode_words(const uint32_t* src,
                                              uint32_t count_words, uint32_t rmax,
                                              float eb, uint32_t rate, uint32_t* out,
-                                             uint32_t (*park)[kThreads],
-                                             const uint32_t* pre = nullptr) {
+                                             uint32_t (*park)[kThreads]) {
     const int tid = threadIdx.x;
     const float eb2 = eb * 2.0f;
+    if (!kWide && kEb2) {
+        // Rates <= 15: the sign word and planes 0..14 make 16 rows.  Fed to
+        // the transpose as rows 15, 0, 1, .., 14 (words w_0, w_1, .., w_15),
+        // they give each element the 16-bit field (sign << 15) | |q|, so q
+        // fits int16 and both halves of a row are turned into q at once with
+        // packed 16-bit operations: q = (|q| ^ -sign) - (-sign), where -sign
+        // is the field shifted right arithmetically by 15.  A zero-rate block
+        // has all words 0, so q = 0 and y = +0.0 (eb2 is finite here).
+        uint32_t W[16], L[16];
+        load_words<16>(src, W, count_words < 16u ? count_words : 16u,
+                       rmax < 15u ? rmax + 1u : 16u);
+#pragma unroll
+        for (int b = 0; b < 16; ++b) L[b] = W[(b + 1) & 15];
+        transpose16x2(L);  // L[k]: fields of elements k^7 (low), 16+(k^7) (high)
+        // Rows k0 = (2j)^7 and k1 = (2j+1)^7 hold elements 2j, 2j+1 (low
+        // halves -> out[j]) and 16+2j, 17+2j (high halves -> out[j + 8]).
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k0 = (2 * j) ^ 7, k1 = (2 * j + 1) ^ 7;
+            uint32_t Q[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t f = L[h ? k1 : k0];
+                const uint32_t ns = __builtin_bit_cast(
+                    uint32_t, __builtin_bit_cast(s16x2, f) >> (short)15);
+                Q[h] = __builtin_bit_cast(
+                    uint32_t, (u16x2)(__builtin_bit_cast(u16x2, (f & 0x7FFF7FFFu) ^ ns) -
+                                      __builtin_bit_cast(u16x2, ns)));
+            }
+            f32x2 y;
+            y.x = (float)(int32_t)(int16_t)(Q[0] & 0xFFFFu) * eb2;
+            y.y = (float)(int32_t)(int16_t)(Q[1] & 0xFFFFu) * eb2;
+            out[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2));
+            y.x = (float)((int32_t)Q[0] >> 16) * eb2;
+            y.y = (float)((int32_t)Q[1] >> 16) * eb2;
+            out[j + 8] = __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2));
+        }
+        return;
+    }
     if (kWide) {
         uint32_t H[16];
         load_words<16>(src + 16, H, count_words > 16u ? count_words - 16u : 0u,
@@ -1366,14 +1403,9 @@ __device__ __forceinline__ void decode_words(const uint32_t* src,
         __asm__ volatile("" ::: "memory");
     }
     uint32_t L[16];
-    if (kPre) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) L[k] = pre[k];
-    } else {
-        load_words<16>(src, L, count_words < 16u ? count_words : 16u,
-                       rmax < 15u ? rmax + 1u : 16u);
-    }
-    transpose16x2(L);  // L[k]: low fields of elements k^7, 16+(k^7)
+    load_words<16>(src, L, count_words < 16u ? count_words : 16u,
+                   rmax < 15u ? rmax + 1u : 16u);
+    transpose16x2(L);  // L[k]: low fields ((|q| << 1) | sign) & 0xFFFF
     // out[i] holds elements 2i and 2i+1.  Rows k0, k1 feed both out[j]
     // (low halves) and out[j + 8] (high halves), so they are consumed
     // together.
@@ -1435,51 +1467,155 @@ __device__ __forceinline__ void decode_block(const uint8_t* in, uint64_t base,
     }
 }
 
-// Writes one decoded block to its destination (cu:539-606): contiguous page,
-// multi-destination split, or layer-indexed position in the full page.
+// Destination of this thread's decoded block when its `count` values go to
+// one contiguous run (cu:539-606: contiguous page, multi-destination split,
+// or layer-indexed position in the full page); nullptr when they do not (or
+// the layer index is bad, which sets `badl`).
+template <int kDst>
+__device__ __forceinline__ uint16_t* block_dst(const DecompressParams& p,
+                                               const Group& g, const DecompressJob& J,
+                                               uint32_t job, uint32_t tile, int tid,
+                                               uint64_t e0, uint32_t count,
+                                               uint32_t& badl) {
+    if (kDst == kDstLinear) return J.dst + e0;
+    if (kDst == kDstMulti) {
+        const uint64_t epd = p.elements_per_dest;
+        const uint64_t di = e0 / epd;
+        const uint64_t off = e0 - di * epd;
+        if (off + count > epd) return nullptr;
+        return p.dests[(uint64_t)job * p.dests_per_page + di] + off;
+    }
+    const LayerCursor c = layer_cursor(g, (uint64_t)tile * kTileElems,
+                                       (uint32_t)tid * kBlockElems, &badl);
+    return (c.contiguous && !badl) ? J.dst + c.src_index : nullptr;
+}
+
+// Value by value, for a block that straddles destinations or layers.
+template <int kDst>
+__device__ __forceinline__ void store_elementwise(const DecompressParams& p,
+                                                  const Group& g, const DecompressJob& J,
+                                                  uint32_t job, uint64_t e0,
+                                                  uint32_t count, const uint32_t* out,
+                                                  uint32_t& badl) {
+    for (uint32_t v = 0; v < count; ++v) {
+        const uint16_t y = (uint16_t)((v & 1) ? (out[v >> 1] >> 16) : (out[v >> 1] & 0xFFFFu));
+        const uint64_t e = e0 + v;
+        if (kDst == kDstMulti) {
+            const uint64_t epd = p.elements_per_dest;
+            const uint64_t dv = e / epd;
+            to_global(p.dests[(uint64_t)job * p.dests_per_page + dv])[e - dv * epd] = y;
+        } else if (kDst == kDstIndexed) {
+            const uint64_t s = map_index(e, g.layers, g.selected_layers,
+                                         g.source_layers, g.elements_per_layer, &badl);
+            if (badl) break;
+            to_global(J.dst)[s] = y;
+        } else {
+            to_global(J.dst)[e] = y;
+        }
+    }
+}
+
+// Each lane writes its own decoded block (cu:539-606).
+template <int kDst>
+__device__ __forceinline__ void store_block_lane(const DecompressParams& p,
+                                                 const Group& g, const DecompressJob& J,
+                                                 uint32_t job, uint32_t tile, int tid,
+                                                 uint64_t e0, uint32_t count,
+                                                 const uint32_t* out, uint32_t& err) {
+    uint32_t badl = 0;
+    uint16_t* dst = block_dst<kDst>(p, g, J, job, tile, tid, e0, count, badl);
+    if (dst != nullptr)
+        store_block(dst, out, count, ((uintptr_t)dst & 15u) == 0);
+    else
+        store_elementwise<kDst>(p, g, J, job, e0, count, out, badl);
+    if (badl) err |= kErrLayerIndex;
+}
+
+// Destination of the 2048 values of wave `wave` of a tile when they are 64
+// whole blocks landing on one contiguous, 16-byte-aligned run; nullptr
+// otherwise (then each lane stores its own block).  Wave-uniform: scalar
+// arithmetic (every index here is below 2^29, the largest segment).
+template <int kDst>
+__device__ __forceinline__ uint16_t* wave_run_dst(const DecompressParams& p,
+                                                  const Group& g, const DecompressJob& J,
+                                                  uint32_t job, uint32_t tile, int wave) {
+    constexpr uint32_t kRun = 64u * kBlockElems;
+    const uint32_t E = tile * (uint32_t)kTileElems + (uint32_t)wave * kRun;
+    if ((uint64_t)E + kRun > g.n) return nullptr;
+    uint16_t* d;
+    if (kDst == kDstLinear) {
+        if (!p.aligned16) return nullptr;
+        d = J.dst + E;
+    } else if (kDst == kDstMulti) {
+        const uint32_t epd = (uint32_t)p.elements_per_dest;
+        const uint32_t di = E / epd, off = E - di * epd;
+        if (off + kRun > epd) return nullptr;
+        d = load_const(p.dests, (uint32_t)(job * p.dests_per_page + di)) + off;
+    } else {
+        const uint32_t epl = (uint32_t)g.elements_per_layer;
+        const uint32_t per_prefix = (uint32_t)g.selected_layers * epl;
+        const uint32_t pre = E / per_prefix;
+        const uint32_t within = E - pre * per_prefix;
+        const uint32_t layer = within / epl;
+        const uint32_t inner = within - layer * epl;
+        if (inner + kRun > epl) return nullptr;
+        const int64_t l = load_const(g.layers, layer);
+        if (l < 0 || (uint64_t)l >= g.source_layers) return nullptr;
+        d = J.dst + (((uint64_t)pre * g.source_layers + (uint64_t)l) * epl + inner);
+    }
+    return ((uintptr_t)d & 15u) ? nullptr : d;
+}
+
+// Writes the wave's 64 decoded blocks to `run` as four fully coalesced 1 KiB
+// stores through the wave's own LDS cells `stage` (lane-strided 64-byte
+// stores reach only about half the write bandwidth of coalesced ones on
+// MI355X).  Staging layout: 16-byte slot j of the wave is the 4 dwords at
+// stage[(j >> 4) * kThreads + 4 * (j & 15)] (the wave's 64-dword column
+// range of row j >> 4); chunk q (dwords 4q..4q+3) of block b is kept in slot
+// 64q + (b ^ 4q), which keeps both the per-block writes and the coalesced
+// reads free of bank conflicts.
+__device__ __forceinline__ void store_wave_run(uint16_t* run, const uint32_t* out,
+                                               uint32_t* stage, int lane) {
+    __asm__ volatile("" ::: "memory");  // after any parked-row reads
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t j = 64u * q + ((uint32_t)lane ^ (4u * q));
+        u32x4 v;
+        v.x = out[4 * q + 0];
+        v.y = out[4 * q + 1];
+        v.z = out[4 * q + 2];
+        v.w = out[4 * q + 3];
+        *reinterpret_cast<u32x4*>(stage + (j >> 4) * kThreads + 4u * (j & 15u)) = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __asm__ volatile("" ::: "memory");
+    g_u32x4* d = (g_u32x4*)to_global(reinterpret_cast<uint32_t*>(run));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t b = 16u * i + ((uint32_t)lane >> 2), q = (uint32_t)lane & 3u;
+        const uint32_t j = 64u * q + (b ^ (4u * q));
+        d[64 * i + lane] =
+            *reinterpret_cast<const u32x4*>(stage + (j >> 4) * kThreads + 4u * (j & 15u));
+    }
+    __builtin_amdgcn_wave_barrier();
+    __asm__ volatile("" ::: "memory");  // before the cells are reused
+}
+
+// Writes the decoded blocks of the wave.  Every lane of the wave calls it;
+// `run` is wave_run_dst's result, `write` whether this lane's block is
+// written (rate-0 blocks are skipped under the reference's policy).
 template <int kDst>
 __device__ __forceinline__ void store_decoded(const DecompressParams& p,
                                               const Group& g, const DecompressJob& J,
                                               uint32_t job, uint32_t tile, int tid,
-                                              uint64_t e0, uint32_t count,
-                                              const uint32_t* out, uint32_t& err) {
-    if (kDst == kDstLinear) {
-        store_block(J.dst + e0, out, count, p.aligned16 != 0);
-    } else if (kDst == kDstMulti) {
-        const uint64_t epd = p.elements_per_dest;
-        const uint64_t di = e0 / epd;
-        const uint64_t off = e0 - di * epd;
-        if (off + count <= epd) {
-            uint16_t* dst = p.dests[(uint64_t)job * p.dests_per_page + di] + off;
-            store_block(dst, out, count, ((uintptr_t)dst & 15u) == 0);
-        } else {
-            for (uint32_t v = 0; v < count; ++v) {
-                const uint64_t e = e0 + v;
-                const uint64_t dv = e / epd;
-                uint16_t* dst = p.dests[(uint64_t)job * p.dests_per_page + dv];
-                to_global(dst)[e - dv * epd] = (uint16_t)((v & 1) ? (out[v >> 1] >> 16)
-                                                       : (out[v >> 1] & 0xFFFFu));
-            }
-        }
-    } else {
-        uint32_t badl = 0;
-        const LayerCursor c = layer_cursor(g, (uint64_t)tile * kTileElems,
-                                           (uint32_t)tid * kBlockElems, &badl);
-        if (c.contiguous && !badl) {
-            uint16_t* dst = J.dst + c.src_index;
-            store_block(dst, out, count, ((uintptr_t)dst & 15u) == 0);
-        } else {
-            for (uint32_t v = 0; v < count; ++v) {
-                const uint64_t s = map_index(e0 + v, g.layers, g.selected_layers,
-                                             g.source_layers, g.elements_per_layer,
-                                             &badl);
-                if (badl) break;
-                to_global(J.dst)[s] = (uint16_t)((v & 1) ? (out[v >> 1] >> 16)
-                                              : (out[v >> 1] & 0xFFFFu));
-            }
-        }
-        if (badl) err |= kErrLayerIndex;
+                                              uint64_t e0, uint32_t count, bool write,
+                                              uint16_t* run, const uint32_t* out,
+                                              uint32_t* stage, uint32_t& err) {
+    if (run != nullptr && __ballot(!write) == 0ull) {
+        store_wave_run(run, out, stage, tid & 63);
+        return;
     }
+    if (write) store_block_lane<kDst>(p, g, J, job, tile, tid, e0, count, out, err);
 }
 
 template <int kDst>
@@ -1488,13 +1624,12 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     __shared__ uint32_t s_tile;
     __shared__ uint32_t s_wave[kThreads / 64];
     __shared__ uint32_t s_prefix;
-    __shared__ uint32_t s_pre[kThreads / 64];
     __shared__ uint32_t s_hdr[kTileBlocks / 4];
     __shared__ uint32_t s_park[16][kThreads];  // wide-rate decode scratch
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     publish_seq(p.host_ctl, p.seq);
     const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {
@@ -1526,40 +1661,16 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
         rate = 0;
     }
     const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
-    // Offset of this tile's payload in the job's stream.  The first tiles
-    // of a job add up the rate bytes of all earlier blocks straight from the
-    // header (cu:410-470 re-derives offsets from the header too), so they
-    // wait for no other workgroup; later tiles use the decoupled look-back,
-    // which stops at the nearest tile that published its inclusive prefix.
-    const bool direct = tile <= kDirectPrefixTiles;
-    if (direct) {
-        uint32_t part = 0;
-        const uint32_t* hw = reinterpret_cast<const uint32_t*>(J.in);
-        for (uint32_t i = tid; i < tile * (kTileBlocks / 4); i += kThreads)
-            part += header_word_bytes(to_global(hw)[i]);
-        part = wave_sum(part);
-        if (lane == 0) s_pre[wave] = part;
-    }
+    // Offset of this tile's payload in the job's stream: decoupled look-back
+    // over the earlier tiles of the job (tile 0 publishes right away).
     const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
-    uint32_t prefix;
-    if (direct) {
-        prefix = 0;
-#pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) prefix += s_pre[w];
-        if (tid == 0 && g.tiles_per_job > kDirectPrefixTiles + 1)
-            store_relaxed(&p.tile_state[t],
-                          ((unsigned long long)(p.epoch * 4u + 2u) << 32) |
-                              (prefix + sc.total));
-    } else {
-        if (wave == 0) {
-            const uint32_t pf = lookback(p.tile_state, t, tile, sc.total,
-                                         p.epoch, p.error, p.host_ctl);
-            if (lane == 0) s_prefix = pf;
-        }
-        __syncthreads();
-        prefix = s_prefix;
+    if (wave == 0) {
+        const uint32_t pf = lookback(p.tile_state, t, tile, sc.total,
+                                     p.epoch, p.error, p.host_ctl);
+        if (lane == 0) s_prefix = pf;
     }
-    const uint64_t base = (uint64_t)R + prefix + sc.exclusive;
+    __syncthreads();
+    const uint64_t base = (uint64_t)R + s_prefix + sc.exclusive;
     if (rate && base + bytes > J.size) {
         err |= kErrTruncated;
         rate = 0;
@@ -1570,73 +1681,114 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     const uint32_t rmax = wave_max(rate);
     uint32_t out[16];
     decode_block(J.in, base, rate, rmax, J.eb, out, s_park);
-    if (count && (rate != 0 || p.rate0_zero))
-        store_decoded<kDst>(p, g, J, job, tile, tid, e0, count, out, err);
+    store_decoded<kDst>(p, g, J, job, tile, tid, e0, count,
+                        count != 0 && (rate != 0 || p.rate0_zero),
+                        wave_run_dst<kDst>(p, g, J, job, tile, wave), out,
+                        &s_park[0][64 * wave], err);
     if (err) flag_error(p.error, p.host_ctl, err);
 }
 
-// Persistent decoder for launches whose jobs have at most
-// kDirectPrefixTiles + 1 tiles (every tile's offset comes from the header,
-// so no workgroup waits for another).  Workgroup w decodes tiles w, w + G,
-// ...; the header words the next tile needs (its own rates and the rate
-// bytes of its job's earlier tiles) are requested before the current tile's
-// payload is decoded, so their latency overlaps the current tile's.  (A
-// deeper pipeline that also prefetches the next payload holds ~90 VGPRs and
-// measured slower at the lower occupancy.)
+// ---- persistent decoder ----------------------------------------------------
+//
+// Workgroup w decodes the consecutive tiles [w*T/G, (w+1)*T/G) of the launch
+// (T tiles over all groups and jobs, G = gridDim.x).  A tile's payload
+// offset is the running sum of the payload bytes of the earlier tiles of its
+// job: the first tile of a workgroup's run adds up the rate bytes of the
+// earlier tiles' headers once (cu:410-470 re-derives offsets from the header
+// too), every following tile adds the previous tile's total, and a tile 0
+// starts from 0.  No workgroup waits for another, for any job length.  The
+// next tile's rate bytes are requested before the current tile is decoded
+// and have arrived before its stores are issued (stores count in the same
+// in-order memory counter, so a wait placed after them would also wait for
+// the stores).
+
+struct DecTile {
+    int gi;         // group
+    uint32_t job;   // job index
+    uint32_t tile;  // tile within the job
+};
+
+__device__ __forceinline__ DecTile dec_tile(const DecompressParams& p, uint32_t t,
+                                            const uint32_t* s_gfirst) {
+    DecTile c;
+    int gi = 0;
+    for (int i = 1; i < p.num_groups; ++i)
+        if (t >= s_gfirst[i]) gi = i;
+    c.gi = __builtin_amdgcn_readfirstlane(gi);
+    const Group& g = p.groups[c.gi];
+    const uint32_t local = t - g.first_tile;
+    const uint32_t jig = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
+    c.tile = local - jig * g.tiles_per_job;
+    c.job = g.first_job + jig;
+    return c;
+}
+
+// This thread's word of a tile's rate bytes (threads < 64).
+__device__ __forceinline__ uint32_t tile_header_word(const uint8_t* in, uint32_t tile,
+                                                     int tid) {
+    return tid < kTileBlocks / 4
+               ? to_global(reinterpret_cast<const uint32_t*>(in))[tile * (kTileBlocks / 4) + tid]
+               : 0u;
+}
+
+// Payload bytes of the tiles [0, tile) of a job, from their rate bytes
+// (whole workgroup, one barrier; s_red holds one word per wave).
+__device__ __forceinline__ uint32_t header_prefix(const uint8_t* in, uint32_t tile,
+                                                  int tid, uint32_t* s_red) {
+    const g_u32* hw = to_global(reinterpret_cast<const uint32_t*>(in));
+    uint32_t part = 0;
+    for (uint32_t i = (uint32_t)tid; i < tile * (kTileBlocks / 4); i += kThreads)
+        part += header_word_bytes(hw[i]);
+    part = wave_sum(part);
+    if ((tid & 63) == 0) s_red[tid >> 6] = part;
+    __syncthreads();
+    uint32_t total = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) total += s_red[w];
+    return total;
+}
+
 template <int kDst>
-__global__ __launch_bounds__(kThreads) void decompress_pipelined_kernel(
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_persistent_kernel(
     DecompressParams p) {
-    constexpr int kPreWords = (int)(kDirectPrefixTiles * (kTileBlocks / 4) / kThreads);
     __shared__ uint32_t s_wave[kThreads / 64];
-    __shared__ uint32_t s_pre[kThreads / 64];
+    __shared__ uint32_t s_red[kThreads / 64];
     __shared__ uint32_t s_hdr[kTileBlocks / 4];
-    __shared__ uint32_t s_park[16][kThreads];  // wide-rate decode scratch
+    __shared__ uint32_t s_gfirst[kMaxGroups];
+    __shared__ uint32_t s_park[16][kThreads];  // wide-rate scratch, store staging
 
     publish_seq(p.host_ctl, p.seq);
-    const Group& g = p.groups[0];
+    if ((int)threadIdx.x < p.num_groups) s_gfirst[threadIdx.x] = p.groups[threadIdx.x].first_tile;
+    __syncthreads();
     const uint32_t G = gridDim.x;
-    const uint32_t tpj = g.tiles_per_job;
-    const uint64_t n = g.n;
-    const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
-    const uint32_t R = g.header_bytes;
+    const uint32_t t_begin = (uint32_t)((uint64_t)blockIdx.x * p.total_tiles / G);
+    const uint32_t t_end = (uint32_t)((uint64_t)(blockIdx.x + 1) * p.total_tiles / G);
+    if (t_begin >= t_end) return;  // whole workgroup
     uint32_t err = 0;
 
-    // Header words of tile tt: this thread's word of the tile's own rates
-    // (threads < 64) and its share of the earlier tiles' rate words.
-    uint32_t hw = 0, pw[kPreWords];
-    auto request_header = [&](uint32_t tt, int tid) {
-        const uint32_t job = tt / tpj, tile = tt - job * tpj;
-        const uint32_t* words = reinterpret_cast<const uint32_t*>(load_const(p.jobs, job).in);
-        hw = tid < kTileBlocks / 4 ? to_global(words)[tile * (kTileBlocks / 4) + tid] : 0u;
-#pragma unroll
-        for (int i = 0; i < kPreWords; ++i) {
-            const uint32_t k = (uint32_t)(tid + i * kThreads);
-            pw[i] = k < tile * (kTileBlocks / 4) ? to_global(words)[k] : 0u;
-        }
-    };
-
-    uint32_t t = blockIdx.x;
-    request_header(t, (int)threadIdx.x);
-    for (;;) {
+    DecTile cur = dec_tile(p, t_begin, s_gfirst);
+    uint32_t prefix = 0;
+    uint32_t hw;
+    {
+        const int tid = (int)threadIdx.x;
+        const uint8_t* in = load_const(p.jobs, cur.job).in;
+        if (cur.tile != 0) prefix = header_prefix(in, cur.tile, tid, s_red);
+        hw = tile_header_word(in, cur.tile, tid);
+    }
+    for (uint32_t t = t_begin;;) {
         const int tid = loop_tid();
-        const int lane = tid & 63;
-        const int wave = tid >> 6;
-        const uint32_t job = t / tpj, tile = t - job * tpj;
-        const DecompressJob J = load_const(p.jobs, job);
-        const uint32_t b = tile * kTileBlocks + tid;
-        const uint64_t e0 = (uint64_t)b * kBlockElems;
-        const uint32_t count =
-            b < nb ? (uint32_t)(n - e0 < kBlockElems ? n - e0 : kBlockElems) : 0u;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const Group& g = p.groups[cur.gi];
+        const DecompressJob J = load_const(p.jobs, cur.job);
+        // Segments hold fewer than 2^29 values: 32-bit element indices.
+        const uint32_t n = (uint32_t)g.n;
+        const uint32_t e0 = (cur.tile * kTileBlocks + (uint32_t)tid) * kBlockElems;
+        const uint32_t count = e0 < n ? (n - e0 < kBlockElems ? n - e0 : kBlockElems) : 0u;
 
-        // Rates (cu:410-418; padding bytes masked) and the earlier tiles'
-        // payload bytes from the words requested last iteration.
+        // Rates (cu:410-418; padding bytes masked), tile scan, offsets.
         if (tid < kTileBlocks / 4) s_hdr[tid] = hw;
         __syncthreads();
-        uint32_t part = 0;
-#pragma unroll
-        for (int i = 0; i < kPreWords; ++i) part += header_word_bytes(pw[i]);
-        part = wave_sum(part);
-        if (lane == 0) s_pre[wave] = part;
         uint32_t rate = count ? (s_hdr[tid >> 2] >> (8 * (tid & 3))) & 0xFFu : 0u;
         if (rate > 31u) {
             err |= kErrRate;
@@ -1644,26 +1796,31 @@ __global__ __launch_bounds__(kThreads) void decompress_pipelined_kernel(
         }
         const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
         const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
-        uint32_t prefix = 0;
-#pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) prefix += s_pre[w];
-        const uint64_t base = (uint64_t)R + prefix + sc.exclusive;
+        const uint64_t base = (uint64_t)g.header_bytes + prefix + sc.exclusive;
         if (rate && base + bytes > J.size) {
             err |= kErrTruncated;
             rate = 0;
         }
 
-        // Ask for the next tile's header words, then decode this tile.
-        const bool has_next = t + G < p.total_tiles;
-        if (has_next) request_header(t + G, tid);
-
+        // Ask for the next tile's rate bytes, then decode this tile.
+        const bool has_next = t + 1 < t_end;
+        DecTile nxt = cur;
+        if (has_next) {
+            nxt = dec_tile(p, t + 1, s_gfirst);
+            hw = tile_header_word(load_const(p.jobs, nxt.job).in, nxt.tile, tid);
+        }
         const uint32_t rmax = wave_max(rate);
+        uint16_t* run = wave_run_dst<kDst>(p, g, J, cur.job, cur.tile, wave);
         uint32_t out[16];
         decode_block(J.in, base, rate, rmax, J.eb, out, s_park);
-        if (count && (rate != 0 || p.rate0_zero))
-            store_decoded<kDst>(p, g, J, job, tile, tid, e0, count, out, err);
+        __asm__ volatile("" ::"v"(hw));  // arrived before the stores are issued
+        store_decoded<kDst>(p, g, J, cur.job, cur.tile, tid, e0, count,
+                            count != 0 && (rate != 0 || p.rate0_zero), run, out,
+                            &s_park[0][64 * wave], err);
         if (!has_next) break;
-        t += G;
+        prefix = nxt.tile == 0 ? 0u : prefix + sc.total;
+        cur = nxt;
+        ++t;
     }
     if (err) flag_error(p.error, p.host_ctl, err);
 }
@@ -1707,18 +1864,18 @@ hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
     return hipGetLastError();
 }
 
-hipError_t launch_decompress_pipelined(const DecompressParams& p, uint32_t grid,
+hipError_t launch_decompress_persistent(const DecompressParams& p, uint32_t grid,
                                        hipStream_t stream, hipEvent_t start,
                                        hipEvent_t stop) {
     switch (p.dst_kind) {
     case kDstMulti:
-        launch(decompress_pipelined_kernel<kDstMulti>, grid, stream, start, stop, p);
+        launch(decompress_persistent_kernel<kDstMulti>, grid, stream, start, stop, p);
         break;
     case kDstIndexed:
-        launch(decompress_pipelined_kernel<kDstIndexed>, grid, stream, start, stop, p);
+        launch(decompress_persistent_kernel<kDstIndexed>, grid, stream, start, stop, p);
         break;
     default:
-        launch(decompress_pipelined_kernel<kDstLinear>, grid, stream, start, stop, p);
+        launch(decompress_persistent_kernel<kDstLinear>, grid, stream, start, stop, p);
         break;
     }
     return hipGetLastError();
@@ -1727,7 +1884,7 @@ hipError_t launch_decompress_pipelined(const DecompressParams& p, uint32_t grid,
 int decompress_resident_workgroups(int device) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(decompress_pipelined_kernel<kDstIndexed>),
+            &per_cu, reinterpret_cast<const void*>(decompress_persistent_kernel<kDstIndexed>),
             kThreads, 0) != hipSuccess)
         per_cu = 1;
     hipDeviceProp_t prop;

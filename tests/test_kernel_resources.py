@@ -63,7 +63,7 @@ def pick(meta, name):
 
 
 def test_persistent_decoder_fits_eight_waves(kernels):
-    for k, m in pick(kernels, "decompress_pipelined_kernel").items():
+    for k, m in pick(kernels, "decompress_persistent_kernel").items():
         assert m["vgpr"] <= 64, (k, m)
         assert m["sgpr"] <= 74, (k, m)
         assert m["lds"] <= 20480, (k, m)
