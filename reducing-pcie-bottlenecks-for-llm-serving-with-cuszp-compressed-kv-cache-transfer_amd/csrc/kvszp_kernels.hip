@@ -872,26 +872,33 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     }
 }
 
-// ---- persistent, software-pipelined encoder --------------------------------
+// ---- persistent encoder ----------------------------------------------------
 //
 // For launches whose blocks are all whole, inside one layer and 16-byte
 // aligned (every segment length and layer length a multiple of 32 values,
 // every page 16-byte aligned) -- the shape of KV pages.  Workgroup w encodes
 // tiles w, w + G, w + 2G, ... (G = gridDim.x, at most the number of
-// co-resident workgroups).  While tile t waits on other tiles -- the
-// relative-bound exchange and the offset look-back -- the blocks of its next
-// tile are already on their way into LDS, and that tile's min/max is
-// published before this tile's look-back wait.  Per iteration:
-//   a. exchange: min/max of all tiles of t's job -> bound
-//   b. quantize t (registers) -> fields, rates
-//   c. tile scan, header bytes, publish t's aggregate
-//   d. next tile: min/max from its LDS copy, published
-//   e. look-back wait -> t's offset
-//   f. payload stores of t
-//   g. next tile's blocks LDS -> registers; start the copy of the one after
-// Every wait of tile t is on a publish that happens before any wait of a
-// lower "rank" (2t for a, 2t+1 for e) once tiles_per_job <= G, so with all G
-// workgroups resident no cycle of waits exists.  All waits are bounded.
+// co-resident workgroups), one 32-value block per thread held in registers
+// together with the block's min/max keys.  Per tile t:
+//   a. exchange: min/max over all tiles of t's job -> bound, reciprocal
+//   b. rates: while every |x * recip| of a block stays below 2^30 and the block
+//      holds no NaN, the quantizer (cu:10-25) is monotone in x, so the
+//      block's largest |q| -- its rate (cu:221-222) -- is that of its smallest
+//      or largest value: two quantizations per block.  Tile scan, header
+//      bytes (cu:226-229) and t's aggregate follow before any quantizing.
+//   d. look-back -> t's payload offset
+//   c. the next tile (loaded into registers one iteration ago) -> its block
+//      keys and min/max, published
+//   e. quantize t into 16-bit fields, transpose to stream words, stage the
+//      wave's payload in LDS and write it with coalesced 16-byte stores
+//   f. the next tile becomes current; its successor starts loading
+// Wait-for order: the exchange of t needs the min/max of t's job, the
+// look-back of t the aggregates of t's predecessors.  Following what a wait
+// depends on always reaches a strictly earlier tile within at most two steps
+// once a job has at most G/2 tiles (a publish that depends on a wait is the
+// min/max of tile u + G, behind the look-back of u; tiles u + G and u are in
+// different jobs), so with all G workgroups resident no cycle of waits
+// exists.  All waits are bounded.
 
 // threadIdx.x behind an empty asm: values derived from it inside the tile
 // loop are recomputed each iteration instead of being hoisted out of the
@@ -932,103 +939,86 @@ __device__ __forceinline__ TileCtx tile_ctx(const CompressParams& p, uint32_t t,
 
 // Whether this thread's block exists (all existing blocks are whole here).
 __device__ __forceinline__ bool block_exists(const Group& g, uint32_t tile, int tid) {
-    return (uint64_t)(tile * kTileBlocks + tid) * kBlockElems < g.n;
+    return (tile * kTileBlocks + (uint32_t)tid) * kBlockElems < (uint32_t)g.n;
 }
 
-// Source element of this thread's block.
-__device__ __forceinline__ uint64_t block_source(const Group& g, uint32_t tile,
-                                                 int tid, uint32_t* bad) {
-    const uint64_t tile_first = (uint64_t)tile * kTileElems;
-    const uint32_t elem = (uint32_t)tid * kBlockElems;
-    if (g.layers == nullptr) return tile_first + elem;
-    // A tile inside one layer reads the layer map once, as a scalar load: a
-    // vector load would also wait for the stores this wave just issued.
-    const uint64_t per_prefix = g.selected_layers * g.elements_per_layer;
-    const uint64_t t_prefix = tile_first / per_prefix;
-    const uint32_t t_within = (uint32_t)(tile_first - t_prefix * per_prefix);
+// Source element of this thread's block.  A wave's 64 blocks inside one
+// layer are placed with wave-uniform (scalar) arithmetic and one scalar load
+// of the layer map; otherwise each lane maps its own block.  Element indices
+// of a segment are below 2^29.
+__device__ __forceinline__ uint64_t enc_block_source(const Group& g, uint32_t tile,
+                                                     int wave, int lane, uint32_t* bad) {
+    constexpr uint32_t kRun = 64u * kBlockElems;
+    const uint32_t E = tile * (uint32_t)kTileElems + (uint32_t)wave * kRun;
+    if (g.layers == nullptr) return E + (uint32_t)lane * kBlockElems;
     const uint32_t epl = (uint32_t)g.elements_per_layer;
-    const uint32_t layer = t_within / epl;
-    const uint32_t inner = t_within - layer * epl;
-    if (inner + (uint32_t)kTileElems <= epl) {
+    const uint32_t per_prefix = (uint32_t)g.selected_layers * epl;
+    const uint32_t pre = E / per_prefix;
+    const uint32_t within = E - pre * per_prefix;
+    const uint32_t layer = within / epl;
+    const uint32_t inner = within - layer * epl;
+    if (inner + kRun <= epl) {
         int64_t l = load_const(g.layers, layer);
         if (l < 0 || (uint64_t)l >= g.source_layers) {
             *bad = 1;
             l = 0;
         }
-        return (t_prefix * g.source_layers + (uint64_t)l) * g.elements_per_layer +
-               inner + elem;
+        return ((uint64_t)pre * g.source_layers + (uint64_t)l) * epl + inner +
+               (uint32_t)lane * kBlockElems;
     }
-    return layer_cursor(g, tile_first, elem, bad).src_index;
+    return layer_cursor(g, (uint64_t)tile * kTileElems,
+                        ((uint32_t)wave * 64u + (uint32_t)lane) * kBlockElems, bad)
+        .src_index;
 }
 
-// Starts the asynchronous copy of this thread's block into the wave's LDS
-// slots: lane l's 16-byte chunk c lands at slot 64c + l.
-__device__ __forceinline__ void stage_block(const Group& g, const uint16_t* in,
-                                            uint32_t tile, uint32_t* lds_wave,
-                                            uint32_t* bad, int tid) {
-    if (!block_exists(g, tile, tid)) return;
-    const char* src = reinterpret_cast<const char*>(in + block_source(g, tile, tid, bad));
+// This thread's block (zeros when it does not exist): four 16-byte loads.
+__device__ __forceinline__ void load_block_regs(const TileCtx& c, const Group& g,
+                                                int wave, int lane, uint32_t* d,
+                                                uint32_t* bad) {
+    const bool ex = block_exists(g, c.tile, wave * 64 + lane);
+    const g_u32x4* src = (const g_u32x4*)to_global(
+        c.J.in + (ex ? enc_block_source(g, c.tile, wave, lane, bad) : 0));
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-        __builtin_amdgcn_global_load_lds(
-            (const __attribute__((address_space(1))) void*)(src + 16 * c),
-            (__attribute__((address_space(3))) void*)(lds_wave + 256 * c), 16, 0, 0);
-}
-
-// This thread's staged block, LDS -> registers (zeros if it does not exist).
-__device__ __forceinline__ void staged_block(const uint32_t* lds_wave, bool exists,
-                                             uint32_t* d, int tid) {
-    const u32x4* slots = reinterpret_cast<const u32x4*>(lds_wave);
-    const int lane = tid & 63;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const u32x4 v = exists ? slots[64 * c + lane] : u32x4{0u, 0u, 0u, 0u};
-        d[4 * c + 0] = v.x;
-        d[4 * c + 1] = v.y;
-        d[4 * c + 2] = v.z;
-        d[4 * c + 3] = v.w;
+    for (int i = 0; i < 4; ++i) {
+        const u32x4 v = ex ? src[i] : u32x4{0u, 0u, 0u, 0u};
+        d[4 * i + 0] = v.x;
+        d[4 * i + 1] = v.y;
+        d[4 * i + 2] = v.z;
+        d[4 * i + 3] = v.w;
     }
 }
 
-// Min/max keys of this thread's staged block, 16 bytes at a time from LDS
-// (few registers while the current tile's fields are live).  A block
-// holding a NaN is redone value by value, skipping NaNs (cu:78-79).
-__device__ __forceinline__ void staged_block_minmax(const uint32_t* lds_wave,
-                                                    bool exists, int tid,
-                                                    uint32_t& kmin, uint32_t& kmax) {
-    kmin = kKeyEmptyMin;
-    kmax = kKeyEmptyMax;
-    if (!exists) return;
-    const u32x4* slots = reinterpret_cast<const u32x4*>(lds_wave);
-    const int lane = tid & 63;
+// Block keys packed as (min key << 16) | max key, plus whether the block
+// holds a NaN (fminf/fmaxf skip NaN, cu:78-79; the quantizer does not).
+__device__ __forceinline__ uint32_t block_keys(const uint32_t* d, bool exists,
+                                               uint32_t& nan) {
+    nan = 0;
+    if (!exists) return (kKeyEmptyMin << 16) | kKeyEmptyMax;
     u16x2 mn = {0xFFFFu, 0xFFFFu}, mx = {0u, 0u};
-#pragma unroll 1
-    for (int c = 0; c < 4; ++c) {
-        const u32x4 v = slots[64 * c + lane];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t w = v[i];
-            const uint32_t neg = __builtin_bit_cast(
-                uint32_t, __builtin_bit_cast(s16x2, w) >> (short)15);
-            const u16x2 k = __builtin_bit_cast(u16x2, w ^ (neg | 0x80008000u));
-            mn = __builtin_elementwise_min(mn, k);
-            mx = __builtin_elementwise_max(mx, k);
+    for (int i = 0; i < kBlockElems / 2; ++i) {
+        // key = sign ? ~h : h | 0x8000, for both halves at once
+        const uint32_t neg = __builtin_bit_cast(
+            uint32_t, __builtin_bit_cast(s16x2, d[i]) >> (short)15);
+        const u16x2 k = __builtin_bit_cast(u16x2, d[i] ^ (neg | 0x80008000u));
+        mn = __builtin_elementwise_min(mn, k);
+        mx = __builtin_elementwise_max(mx, k);
+    }
+    uint32_t kmin = mn.x < mn.y ? mn.x : mn.y;
+    uint32_t kmax = mx.x > mx.y ? mx.x : mx.y;
+    if (!(kmin >= 0x007Fu && kmax <= 0xFF80u)) {
+        // NaN keys fall outside [key(-inf), key(+inf)]: redo value by value.
+        nan = 1;
+        float lo = FLT_MAX, hi = -FLT_MAX;
+        for (int v = 0; v < kBlockElems; ++v) {
+            const float x = (v & 1) ? bf16_hi(d[v >> 1]) : bf16_lo(d[v >> 1]);
+            lo = fminf(lo, x);
+            hi = fmaxf(hi, x);
         }
+        kmin = lo == FLT_MAX ? kKeyEmptyMin : bf16_key(lo);
+        kmax = hi == -FLT_MAX ? kKeyEmptyMax : bf16_key(hi);
     }
-    kmin = mn.x < mn.y ? mn.x : mn.y;
-    kmax = mx.x > mx.y ? mx.x : mx.y;
-    if (kmin >= 0x007Fu && kmax <= 0xFF80u) return;
-    const uint32_t* words = lds_wave;
-    float lo = FLT_MAX, hi = -FLT_MAX;
-#pragma unroll 1
-    for (int v = 0; v < kBlockElems; ++v) {
-        const uint32_t w = words[(64 * (v >> 3) + lane) * 4 + ((v >> 1) & 3)];
-        const float x = (v & 1) ? bf16_hi(w) : bf16_lo(w);
-        lo = fminf(lo, x);
-        hi = fmaxf(hi, x);
-    }
-    kmin = lo == FLT_MAX ? kKeyEmptyMin : bf16_key(lo);
-    kmax = hi == -FLT_MAX ? kKeyEmptyMax : bf16_key(hi);
+    return (kmin << 16) | kmax;
 }
 
 // Tile min/max: this thread's keys -> the tile's epoch-tagged word (one
@@ -1094,19 +1084,112 @@ __device__ __forceinline__ void exchange_minmax(const CompressParams& p,
     }
 }
 
-// Six waves per SIMD: at 80 VGPRs the loop body needs no scratch (at 64 or 72
-// it spills, and measured slower than this).
+// Rate of a block from its keys (see b. above; the caller checked that no
+// |x * recip| of the block reaches 2^30 and that it holds no NaN).
+template <int kQuant>
+__device__ __forceinline__ uint32_t rate_from_keys(uint32_t keys, float recip) {
+    const uint32_t m = max(magnitude(quantize<kQuant>(key_value(keys >> 16), recip)),
+                           magnitude(quantize<kQuant>(key_value(keys & 0xFFFFu), recip)));
+    return m ? 32u - (uint32_t)__builtin_clz(m) : 0u;
+}
+
+// Rate of a block by quantizing every value (NaN, saturation, wrap).
+template <int kQuant>
+__device__ __forceinline__ uint32_t rate_by_quantizing(const uint32_t* d, float recip) {
+    uint32_t orv = 0;
+#pragma unroll
+    for (int v = 0; v < kBlockElems; ++v)
+        orv |= magnitude(quant_elem<kQuant, true>(d, v, kBlockElems, recip));
+    return orv ? 32u - (uint32_t)__builtin_clz(orv) : 0u;
+}
+
+// Rows of 16-bit fields (sign << 15) | |q| for a block whose |q| < 2^15 and
+// whose |t| < 2^31 (quant_field's identity): row k holds elements k^7 (low
+// half) and 16+(k^7) (high half).  After transpose16x2, rows 0..14 are planes
+// 0..14 (stream words w_1..w_15) and row 15 is the sign word w_0.  The two-
+// roundings sign test t < 0 is t's sign bit (t is never -0.0: v + 0.5 = 0
+// rounds to +0.0; the caller excludes NaN).  Rows are chained through the
+// block's words (an empty asm) so the scheduler does not start all 32
+// conversions at once.
+template <int kQuant>
+__device__ __forceinline__ void build_rows_signhi(uint32_t* d, float recip, uint32_t* P) {
+    uint32_t prev = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int e0 = row_lo_elem(k), e1 = row_hi_elem(k);
+        asm volatile("" : "+v"(d[e0 >> 1]), "+v"(d[e1 >> 1]) : "v"(prev));
+        const float x0 = (e0 & 1) ? bf16_hi(d[e0 >> 1]) : bf16_lo(d[e0 >> 1]);
+        const float x1 = (e1 & 1) ? bf16_hi(d[e1 >> 1]) : bf16_lo(d[e1 >> 1]);
+        uint32_t f[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float x = h ? x1 : x0;
+            const float t = kQuant ? __builtin_fmaf(x, recip, 0.5f) : x * recip + 0.5f;
+            const uint32_t c = cvt_abs_u32(t);
+            const uint32_t s = kQuant ? (field_sign(t, 1) ? 1u : 0u)
+                                      : __float_as_uint(t) >> 31;
+            f[h] = s * 0x8001u + c;  // (c + s) | (s << 15), one v_mad_u32_u24
+        }
+        P[k] = __builtin_amdgcn_perm(f[1], f[0], 0x05040100u);  // low halves
+        prev = P[k];
+    }
+}
+
+// Stages a wave's payload in LDS and writes it with coalesced stores.
+// Lane l's block occupies words [off, off + count) of the wave's payload,
+// whose first word goes to global dword address `g0` (in units of 4 bytes
+// from address 0); W[0..count) are the block's stream words.  LDS word
+// `shift + i` holds payload word i, with shift = g0 mod 4 so that LDS and
+// global 16-byte groups coincide.  Words are written from the highest index
+// down: a lane's unused slots (index >= count) only ever fall on later lanes'
+// words, which are written afterwards, or past the payload end.  `stage` has
+// room for 1024 + 3 + 16 words.
+__device__ __forceinline__ void stage_and_store(uint32_t* dst_word0, uint32_t g0,
+                                                const uint32_t* W, uint32_t count,
+                                                uint32_t off, uint32_t cmax,
+                                                uint32_t total, uint32_t* stage,
+                                                int lane) {
+    const uint32_t shift = g0 & 3u;
+    __asm__ volatile("" ::: "memory");
+    if (count) {
+        uint32_t* s = stage + shift + off;
+#pragma unroll
+        for (int j = 15; j >= 0; --j)
+            if ((uint32_t)j < cmax) s[j] = W[j];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __asm__ volatile("" ::: "memory");
+    // Group q covers LDS words [4q, 4q + 4) <-> global words dst_word0 - shift + 4q ..
+    g_u32* d = to_global(dst_word0 - shift);
+    const uint32_t groups = (shift + total + 3u) >> 2;
+    for (uint32_t q = (uint32_t)lane; q < groups; q += 64u) {
+        const uint32_t lo = 4u * q;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + lo);
+        if (lo >= shift && lo + 4u <= shift + total) {
+            *(g_u32x4*)(d + lo) = v;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (lo + i >= shift && lo + i < shift + total) d[lo + i] = v[i];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __asm__ volatile("" ::: "memory");  // before the words are reused
+}
+
+// Six waves per SIMD (at most 80 VGPRs).
 template <int kQuant>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(6, 6))) void compress_pipelined_kernel(
+__attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
     CompressParams p) {
+    constexpr int kStageWords = 1024 + 3 + 16 + 5;  // 16-byte multiple per wave
     __shared__ uint32_t s_wave[kThreads / 64];
     __shared__ uint32_t s_min[kThreads / 64], s_max[kThreads / 64];    // publish
     __shared__ uint32_t s_xmin[kThreads / 64], s_xmax[kThreads / 64];  // exchange
     __shared__ uint32_t s_prefix;
     __shared__ uint32_t s_gfirst[kMaxGroups];
     __shared__ uint8_t s_rate[kTileBlocks];
-    __shared__ __attribute__((aligned(16))) uint32_t s_stage[kThreads / 64][1024];
+    __shared__ __attribute__((aligned(16))) uint32_t s_stage[kThreads / 64][kStageWords];
 
     publish_seq(p.host_ctl, p.seq);
     if ((int)threadIdx.x < p.num_groups) s_gfirst[threadIdx.x] = p.groups[threadIdx.x].first_tile;
@@ -1115,71 +1198,56 @@ __attribute__((amdgpu_waves_per_eu(6, 6))) void compress_pipelined_kernel(
     const bool fused = p.bound_mode == kBoundFused;
     uint32_t bad = 0;
 
-    // Prologue: stage the first tile, publish its min/max, stage the next.
+    // Prologue: the first tile and its keys (published), the next one loading.
     TileCtx cur = tile_ctx(p, blockIdx.x, s_gfirst);
-    uint32_t d[16];
+    uint32_t D[16], N[16];
+    uint32_t keys;
+    uint32_t nan;  // 0/1 per lane (a VGPR rather than a lane mask)
     bool has_next;
     TileCtx nxt;
     {
         const int tid = loop_tid();
-        uint32_t* stage = &s_stage[tid >> 6][0];
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const Group& g = p.groups[cur.gi];
-        const bool ex = block_exists(g, cur.tile, tid);
-        stage_block(g, cur.J.in, cur.tile, stage, &bad, tid);
-        __builtin_amdgcn_s_waitcnt(0);
-        staged_block(stage, ex, d, tid);
-        if (fused) {
-            uint32_t kmin, kmax;
-            block_key_minmax(d, ex ? kBlockElems : 0u, kmin, kmax);
-            publish_tile_keys(p, cur.t, kmin, kmax, s_min, s_max, tid);
-        }
-        __builtin_amdgcn_s_waitcnt(0);  // LDS reads done before it is refilled
+        load_block_regs(cur, g, wave, tid & 63, D, &bad);
+        keys = block_keys(D, block_exists(g, cur.tile, tid), nan);
+        if (fused) publish_tile_keys(p, cur.t, keys >> 16, keys & 0xFFFFu, s_min, s_max, tid);
         has_next = cur.t + G < p.total_tiles;
         if (has_next) {
             nxt = tile_ctx(p, cur.t + G, s_gfirst);
-            stage_block(p.groups[nxt.gi], nxt.J.in, nxt.tile, stage, &bad, tid);
+            load_block_regs(nxt, p.groups[nxt.gi], wave, tid & 63, N, &bad);
         }
     }
 
     for (;;) {
         const int tid = loop_tid();
         const int lane = tid & 63;
-        const int wave = tid >> 6;
-        uint32_t* stage = &s_stage[wave][0];
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const Group& g = p.groups[cur.gi];
         const bool ex = block_exists(g, cur.tile, tid);
 
         // a. bound
         float eb = cur.J.eps;
-        float M = FLT_MAX;  // bound on every |x| of the job
         if (fused) {
             uint32_t kmin, kmax;
             exchange_minmax(p, cur.t - cur.tile, g.tiles_per_job, s_xmin, s_xmax,
                             kmin, kmax, tid);
             eb = relative_bound(cur.J.eps, kmin, kmax);
-            M = fmaxf(fabsf(min_key_value(kmin)), fabsf(max_key_value(kmax)));
         }
         const float recip = 0.5f / eb;  // cu:166, IEEE division
-        // Whole fields straight from t when no |t| can reach 2^31.
-        const bool fast = fused && M * recip < 0x1p30f;
 
-        // b. quantize (cu:180-231); a block past the end has d = 0 -> rate 0
-        uint32_t P[16];
-        uint32_t orv = 0;
-        if (fast) {
-            uint32_t orf = 0;
-            build_rows_fast_chained<kQuant>(d, recip, P, orf);
-            orv = orf >> 1;
-        } else {
-            build_rows_lo_chained<kQuant>(d, recip, P, orv);
-        }
-        const uint32_t rate = (ex && orv) ? 32u - (uint32_t)__builtin_clz(orv) : 0u;
+        // b. rates, tile scan, header bytes (padding zeroed by the last
+        // tile), aggregate out; then this tile's fields, so that only the
+        // 16 rows stay live through the look-back
+        const float bmax = fmaxf(fabsf(key_value(keys >> 16)), fabsf(key_value(keys & 0xFFFFu)));
+        const bool mono = !ex || (nan == 0 && fabsf(bmax * recip) < 0x1p30f);
+        const bool wave_mono = __ballot(!mono) == 0ull;  // wave-uniform
+        uint32_t rate = 0;
+        if (ex) rate = wave_mono ? rate_from_keys<kQuant>(keys, recip)
+                                 : rate_by_quantizing<kQuant>(D, recip);
         const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
         s_rate[tid] = (uint8_t)rate;
-
-        // c. scan, header bytes (cu:226-229; padding zeroed by the last
-        // tile), aggregate out
-        const TileScan sc = tile_scan(bytes, tid, s_wave);
+        const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
         const uint32_t R = g.header_bytes;
         if (tid < kTileBlocks / 4) {
             const uint32_t word = (uint32_t)s_rate[4 * tid] |
@@ -1195,17 +1263,32 @@ __attribute__((amdgpu_waves_per_eu(6, 6))) void compress_pipelined_kernel(
                 *to_global(reinterpret_cast<uint32_t*>(cur.J.out + off)) = 0u;
         }
         if (wave == 0) lookback_publish(p.tile_state, cur.t, cur.tile, sc.total, p.epoch);
-
-        // d. next tile's min/max while this tile's predecessors finish
-        if (has_next && fused) {
-            uint32_t kmin, kmax;
-            __builtin_amdgcn_s_waitcnt(0);  // staged LDS writes have landed
-            staged_block_minmax(stage, block_exists(p.groups[nxt.gi], nxt.tile, tid),
-                                tid, kmin, kmax);
-            publish_tile_keys(p, nxt.t, kmin, kmax, s_min, s_max, tid);
+        const uint32_t rmax = wave_max(rate);
+        // Fields (cu:180-231).  signhi: (sign << 15) | |q| rows, whose
+        // transpose gives planes 0..14 then the sign word; otherwise
+        // ((|q| << 1) | sign) & 0xFFFF rows, whose transpose gives the words
+        // in stream order.
+        const bool signhi = wave_mono && rmax <= 15u;
+        uint32_t P[16];
+        if (rmax > 15u) {
+            // Rates 16..31 (rare): the high fields (|q| >> 15: planes 15..30,
+            // words w_16..w_31) are transposed and parked in the wave's
+            // staging words, which this path does not use for staging.
+            build_rows_hi_chained<kQuant>(D, recip, P);
+            transpose16x2(P);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s_stage[wave][64 * j + lane] = P[j];
+        }
+        if (rmax != 0) {
+            if (signhi) {
+                build_rows_signhi<kQuant>(D, recip, P);
+            } else {
+                uint32_t orv = 0;
+                build_rows_lo_chained<kQuant>(D, recip, P, orv);
+            }
         }
 
-        // e. offset
+        // d. offset
         if (wave == 0) {
             const uint32_t prefix = lookback_wait(p.tile_state, cur.t, cur.tile,
                                                   sc.total, p.epoch, p.error,
@@ -1222,44 +1305,61 @@ __attribute__((amdgpu_waves_per_eu(6, 6))) void compress_pipelined_kernel(
         }
         __syncthreads();
 
-        // f. payload (cu:302-358)
-        const uint32_t rmax = wave_max(rate);
+        // c. the next tile's keys and min/max (its loads were issued one
+        // iteration ago and complete here, before this tile's stores)
+        uint32_t nkeys = 0;
+        uint32_t nnan = 0;
+        if (has_next) {
+            nkeys = block_keys(N, block_exists(p.groups[nxt.gi], nxt.tile, tid), nnan);
+            if (fused)
+                publish_tile_keys(p, nxt.t, nkeys >> 16, nkeys & 0xFFFFu, s_min, s_max, tid);
+        }
+
+        // e. payload (cu:302-358): sign word, then `rate` plane words
         if (rmax != 0) {
-            uint32_t* dst = reinterpret_cast<uint32_t*>(cur.J.out + R + s_prefix + sc.exclusive);
-            const uint32_t count_words = rate ? rate + 1u : 0u;
-            transpose16x2(P);
-            store_words<16>(dst, P, count_words < 16u ? count_words : 16u,
-                            rmax < 15u ? rmax + 1u : 16u);
-            if (rmax >= 16u) {
-                // Planes 15..30 (rates 16..31): rare, so the block is re-read
-                // rather than kept in registers across the waits.
-                const g_u32x4* src = (const g_u32x4*)to_global(
-                    cur.J.in + (ex ? block_source(g, cur.tile, tid, &bad) : 0));
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const u32x4 v = ex ? src[i] : u32x4{0u, 0u, 0u, 0u};
-                    d[4 * i + 0] = v.x;
-                    d[4 * i + 1] = v.y;
-                    d[4 * i + 2] = v.z;
-                    d[4 * i + 3] = v.w;
-                }
-                build_rows_hi_chained<kQuant>(d, recip, P);
+            const uint32_t count = rate ? rate + 1u : 0u;
+            uint8_t* base = cur.J.out + R + s_prefix;
+            if (rmax <= 15u) {
+                const uint32_t wave_off = __builtin_amdgcn_readfirstlane(sc.exclusive);
+                uint32_t* wave_dst = reinterpret_cast<uint32_t*>(base + wave_off);
+                const uint32_t g0 = (uint32_t)(reinterpret_cast<uintptr_t>(wave_dst) >> 2);
+                const uint32_t total =
+                    (uint32_t)__builtin_amdgcn_readlane((int)(sc.exclusive + bytes), 63) - wave_off;
                 transpose16x2(P);
-                store_words<16>(dst + 16, P, count_words > 16u ? count_words - 16u : 0u,
-                                rmax - 15u);
+                uint32_t W[16];
+                if (signhi) {
+                    W[0] = P[15];
+#pragma unroll
+                    for (int j = 1; j < 16; ++j) W[j] = P[j - 1];
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) W[j] = P[j];
+                }
+                stage_and_store(wave_dst, g0, W, count, (sc.exclusive - wave_off) >> 2,
+                                rmax + 1u, total >> 2, &s_stage[wave][0], lane);
+            } else {
+                // Rates 16..31 (rare): each lane writes its own words, the
+                // low fields built above, then the parked high fields.
+                uint32_t* dst = reinterpret_cast<uint32_t*>(base + sc.exclusive);
+                transpose16x2(P);
+                store_words<16>(dst, P, count < 16u ? count : 16u, 16u);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) P[j] = s_stage[wave][64 * j + lane];
+                store_words<16>(dst + 16, P, count > 16u ? count - 16u : 0u, rmax - 15u);
             }
         }
 
-        // g. advance
+        // f. advance
         if (!has_next) break;
         cur = nxt;
-        __builtin_amdgcn_s_waitcnt(0);
-        staged_block(stage, block_exists(p.groups[cur.gi], cur.tile, tid), d, tid);
-        __builtin_amdgcn_s_waitcnt(0);  // LDS reads done before it is refilled
+#pragma unroll
+        for (int i = 0; i < 16; ++i) D[i] = N[i];
+        keys = nkeys;
+        nan = nnan;
         has_next = cur.t + G < p.total_tiles;
         if (has_next) {
             nxt = tile_ctx(p, cur.t + G, s_gfirst);
-            stage_block(p.groups[nxt.gi], nxt.J.in, nxt.tile, stage, &bad, tid);
+            load_block_regs(nxt, p.groups[nxt.gi], wave, lane, N, &bad);
         }
     }
     if (bad & 1) flag_error(p.error, p.host_ctl, kErrLayerIndex);
@@ -1852,9 +1952,9 @@ hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
                                      hipStream_t stream, hipEvent_t start,
                                      hipEvent_t stop) {
     if (p.quantizer)
-        launch(compress_pipelined_kernel<1>, grid, stream, start, stop, p);
+        launch(compress_persistent_kernel<1>, grid, stream, start, stop, p);
     else
-        launch(compress_pipelined_kernel<0>, grid, stream, start, stop, p);
+        launch(compress_persistent_kernel<0>, grid, stream, start, stop, p);
     return hipGetLastError();
 }
 
@@ -1911,7 +2011,7 @@ hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
 int compress_resident_workgroups(int device, bool pipelined) {
     int per_cu = 0;
     const void* fn = pipelined
-        ? reinterpret_cast<const void*>(compress_pipelined_kernel<0>)
+        ? reinterpret_cast<const void*>(compress_persistent_kernel<0>)
         : reinterpret_cast<const void*>(compress_kernel<0>);
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0) !=
         hipSuccess)
