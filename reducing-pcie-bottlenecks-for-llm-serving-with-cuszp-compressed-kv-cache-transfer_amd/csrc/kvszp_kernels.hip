@@ -915,8 +915,14 @@ struct TileCtx {
     int gi;         // group
     uint32_t job;   // job index
     uint32_t tile;  // tile within the job
-    CompressJob J;
 };
+
+// The job record of a tile, read where it is needed (scalar loads through
+// the constant cache) rather than carried across the tile loop in scalar
+// registers.
+__device__ __forceinline__ CompressJob job_of(const CompressParams& p, const TileCtx& c) {
+    return load_const(p.jobs, c.job);
+}
 
 // Group lookup from first-tile numbers kept in LDS (a loop over kernel
 // arguments would keep all of them in scalar registers across the tile loop).
@@ -933,7 +939,6 @@ __device__ __forceinline__ TileCtx tile_ctx(const CompressParams& p, uint32_t t,
     const uint32_t jig = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
     c.tile = local - jig * g.tiles_per_job;
     c.job = g.first_job + jig;
-    c.J = load_const(p.jobs, c.job);
     return c;
 }
 
@@ -972,12 +977,12 @@ __device__ __forceinline__ uint64_t enc_block_source(const Group& g, uint32_t ti
 }
 
 // This thread's block (zeros when it does not exist): four 16-byte loads.
-__device__ __forceinline__ void load_block_regs(const TileCtx& c, const Group& g,
-                                                int wave, int lane, uint32_t* d,
-                                                uint32_t* bad) {
+__device__ __forceinline__ void load_block_regs(const CompressParams& p, const TileCtx& c,
+                                                const Group& g, int wave, int lane,
+                                                uint32_t* d, uint32_t* bad) {
     const bool ex = block_exists(g, c.tile, wave * 64 + lane);
     const g_u32x4* src = (const g_u32x4*)to_global(
-        c.J.in + (ex ? enc_block_source(g, c.tile, wave, lane, bad) : 0));
+        job_of(p, c).in + (ex ? enc_block_source(g, c.tile, wave, lane, bad) : 0));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const u32x4 v = ex ? src[i] : u32x4{0u, 0u, 0u, 0u};
@@ -1111,8 +1116,17 @@ __device__ __forceinline__ uint32_t rate_by_quantizing(const uint32_t* d, float 
 // rounds to +0.0; the caller excludes NaN).  Rows are chained through the
 // block's words (an empty asm) so the scheduler does not start all 32
 // conversions at once.
+// a * b + c for a, b < 2^24 as one instruction (the compiler otherwise
+// expands s * 0x8001 for a 0/1 value s into an arithmetic shift and an AND).
+__device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t d;
+    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(b), "v"(c));
+    return d;
+}
+
 template <int kQuant>
 __device__ __forceinline__ void build_rows_signhi(uint32_t* d, float recip, uint32_t* P) {
+    constexpr uint32_t kSignHi = 0x8001u;
     uint32_t prev = 0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -1128,67 +1142,101 @@ __device__ __forceinline__ void build_rows_signhi(uint32_t* d, float recip, uint
             const uint32_t c = cvt_abs_u32(t);
             const uint32_t s = kQuant ? (field_sign(t, 1) ? 1u : 0u)
                                       : __float_as_uint(t) >> 31;
-            f[h] = s * 0x8001u + c;  // (c + s) | (s << 15), one v_mad_u32_u24
+            f[h] = mad_u24(s, kSignHi, c);  // (c + s) | (s << 15)
         }
         P[k] = __builtin_amdgcn_perm(f[1], f[0], 0x05040100u);  // low halves
         prev = P[k];
     }
 }
 
-// Stages a wave's payload in LDS and writes it with coalesced stores.
-// Lane l's block occupies words [off, off + count) of the wave's payload,
-// whose first word goes to global dword address `g0` (in units of 4 bytes
-// from address 0); W[0..count) are the block's stream words.  LDS word
-// `shift + i` holds payload word i, with shift = g0 mod 4 so that LDS and
-// global 16-byte groups coincide.  Words are written from the highest index
-// down: a lane's unused slots (index >= count) only ever fall on later lanes'
-// words, which are written afterwards, or past the payload end.  `stage` has
-// room for 1024 + 3 + 16 words.
-__device__ __forceinline__ void stage_and_store(uint32_t* dst_word0, uint32_t g0,
-                                                const uint32_t* W, uint32_t count,
-                                                uint32_t off, uint32_t cmax,
-                                                uint32_t total, uint32_t* stage,
-                                                int lane) {
-    const uint32_t shift = g0 & 3u;
+// A wave's payload staged in LDS: lane l's block is words [off, off + count)
+// of the wave's payload, W[0..count) its stream words.  Words are written
+// from the highest index down: a lane's unused slots (index >= count) only
+// ever fall on later lanes' words, which are written afterwards, or past the
+// payload end, so `stage` needs room for 1024 + 16 words.
+__device__ __forceinline__ void stage_payload(const uint32_t* W, uint32_t count,
+                                              uint32_t off, uint32_t cmax,
+                                              uint32_t* stage) {
     __asm__ volatile("" ::: "memory");
     if (count) {
-        uint32_t* s = stage + shift + off;
+        uint32_t* s = stage + off;
 #pragma unroll
         for (int j = 15; j >= 0; --j)
             if ((uint32_t)j < cmax) s[j] = W[j];
     }
+    __asm__ volatile("" ::: "memory");
+}
+
+// Writes a wave's staged payload (`words` words) to `dst` (4-byte aligned)
+// with 16-byte stores on 16-byte boundaries: destination group q covers
+// dst[4q - shift .. 4q - shift + 4), shift = (dst / 4) mod 4, i.e. staged
+// words 4q - shift .. ; partial groups at either end are written word by
+// word.
+__device__ __forceinline__ void copy_payload(uint32_t* dst, uint32_t words,
+                                             const uint32_t* stage, int lane) {
     __builtin_amdgcn_wave_barrier();
     __asm__ volatile("" ::: "memory");
-    // Group q covers LDS words [4q, 4q + 4) <-> global words dst_word0 - shift + 4q ..
-    g_u32* d = to_global(dst_word0 - shift);
-    const uint32_t groups = (shift + total + 3u) >> 2;
+    const uint32_t shift = (uint32_t)(reinterpret_cast<uintptr_t>(dst) >> 2) & 3u;
+    g_u32* d = to_global(dst - shift);
+    const uint32_t groups = (shift + words + 3u) >> 2;
     for (uint32_t q = (uint32_t)lane; q < groups; q += 64u) {
-        const uint32_t lo = 4u * q;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + lo);
-        if (lo >= shift && lo + 4u <= shift + total) {
-            *(g_u32x4*)(d + lo) = v;
+        const int32_t lo = (int32_t)(4u * q) - (int32_t)shift;  // staged index of d[4q]
+        if (lo >= 0 && lo + 4 <= (int32_t)words) {
+            u32x4 v;
+            v.x = stage[lo + 0];
+            v.y = stage[lo + 1];
+            v.z = stage[lo + 2];
+            v.w = stage[lo + 3];
+            *(g_u32x4*)(d + 4u * q) = v;
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (lo + i >= shift && lo + i < shift + total) d[lo + i] = v[i];
+                if (lo + i >= 0 && lo + i < (int32_t)words) d[4u * q + i] = stage[lo + i];
         }
     }
     __builtin_amdgcn_wave_barrier();
     __asm__ volatile("" ::: "memory");  // before the words are reused
 }
 
-// Six waves per SIMD (at most 80 VGPRs).
+// Tile-level facts of the tile whose payload waits in the staging words.
+struct PendingTile {
+    uint32_t t, tile, job, total, R, last, first;
+    float eb;
+    uint8_t* out;
+};
+
+// Five waves per SIMD (at most 96 VGPRs, no scratch).
+//
+// Deferred stores: a tile's payload is staged in LDS at wave-relative
+// offsets and written out one iteration later, after the tile's look-back,
+// which by then normally finds its predecessors' prefixes published and does
+// not wait.  The look-back of tile t - G runs in wave 0 before tile t's scan,
+// whose barrier hands the prefix to the other waves.  A tile with a rate
+// above 15 (payload too large to stage) is stored at once instead, after its
+// own look-back.
+//
+// Wait order with deferral (ranks increase along every workgroup's program):
+// the exchange of tile t has rank t, the look-back of t rank t + G + 1/2.
+// The look-back of t needs the aggregates of tiles x < t, published after the
+// exchange of x (rank x) and look-backs of rank <= x - G + 1/2; the exchange of
+// t needs the min/max of tiles u of t's job, published after the exchange of
+// u - G (rank u - G < t, as u < t + G/2) and look-backs of rank <= u - 2G +
+// 1/2.  Every wait depends only on waits of lower rank: no cycle while all
+// G workgroups are resident.
 template <int kQuant>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
     CompressParams p) {
-    constexpr int kStageWords = 1024 + 3 + 16 + 5;  // 16-byte multiple per wave
-    __shared__ uint32_t s_wave[kThreads / 64];
+    constexpr int kStageWords = 1024 + 16;
+    __shared__ uint32_t s_wave[2][kThreads / 64];
+    __shared__ uint32_t s_wmax[2][kThreads / 64];
     __shared__ uint32_t s_min[kThreads / 64], s_max[kThreads / 64];    // publish
     __shared__ uint32_t s_xmin[kThreads / 64], s_xmax[kThreads / 64];  // exchange
-    __shared__ uint32_t s_prefix;
+    __shared__ uint32_t s_prefix[3];  // by tile parity; [2] for the last tile
     __shared__ uint32_t s_gfirst[kMaxGroups];
-    __shared__ uint8_t s_rate[kTileBlocks];
+    __shared__ uint8_t s_rate[2][kTileBlocks];
+    __shared__ PendingTile s_pend[2];  // by the parity of the tile it holds
+    __shared__ uint32_t s_pwave[kThreads / 64][2];  // staged: wave offset, words
     __shared__ __attribute__((aligned(16))) uint32_t s_stage[kThreads / 64][kStageWords];
 
     publish_seq(p.host_ctl, p.seq);
@@ -1197,6 +1245,7 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
     const uint32_t G = gridDim.x;
     const bool fused = p.bound_mode == kBoundFused;
     uint32_t bad = 0;
+    bool pending = false;  // a tile's payload waits in the staging words
 
     // Prologue: the first tile and its keys (published), the next one loading.
     TileCtx cur = tile_ctx(p, blockIdx.x, s_gfirst);
@@ -1209,36 +1258,50 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         const int tid = loop_tid();
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const Group& g = p.groups[cur.gi];
-        load_block_regs(cur, g, wave, tid & 63, D, &bad);
+        load_block_regs(p, cur, g, wave, tid & 63, D, &bad);
         keys = block_keys(D, block_exists(g, cur.tile, tid), nan);
         if (fused) publish_tile_keys(p, cur.t, keys >> 16, keys & 0xFFFFu, s_min, s_max, tid);
         has_next = cur.t + G < p.total_tiles;
         if (has_next) {
             nxt = tile_ctx(p, cur.t + G, s_gfirst);
-            load_block_regs(nxt, p.groups[nxt.gi], wave, tid & 63, N, &bad);
+            load_block_regs(p, nxt, p.groups[nxt.gi], wave, tid & 63, N, &bad);
         }
     }
 
-    for (;;) {
+    uint32_t parity = 0;
+    for (;; parity ^= 1u) {
         const int tid = loop_tid();
         const int lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const Group& g = p.groups[cur.gi];
         const bool ex = block_exists(g, cur.tile, tid);
 
-        // a. bound
-        float eb = cur.J.eps;
+        // a. bound; wave 0 also finishes the pending tile's look-back
+        float eb = job_of(p, cur).eps;
         if (fused) {
             uint32_t kmin, kmax;
             exchange_minmax(p, cur.t - cur.tile, g.tiles_per_job, s_xmin, s_xmax,
                             kmin, kmax, tid);
-            eb = relative_bound(cur.J.eps, kmin, kmax);
+            eb = relative_bound(job_of(p, cur).eps, kmin, kmax);
         }
         const float recip = 0.5f / eb;  // cu:166, IEEE division
+        if (pending && wave == 0) {
+            const PendingTile& q = s_pend[parity ^ 1u];
+            const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
+                                              p.epoch, p.error, p.host_ctl);
+            if (lane == 0) {
+                s_prefix[parity] = pf;
+                if (q.last)
+                    __hip_atomic_store(&p.host_sizes[q.job], q.R + pf + q.total,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (q.first)
+                    __hip_atomic_store(&p.host_bounds[q.job], q.eb, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
 
         // b. rates, tile scan, header bytes (padding zeroed by the last
-        // tile), aggregate out; then this tile's fields, so that only the
-        // 16 rows stay live through the look-back
+        // tile), aggregate out
         const float bmax = fmaxf(fabsf(key_value(keys >> 16)), fabsf(key_value(keys & 0xFFFFu)));
         const bool mono = !ex || (nan == 0 && fabsf(bmax * recip) < 0x1p30f);
         const bool wave_mono = __ballot(!mono) == 0ull;  // wave-uniform
@@ -1246,24 +1309,39 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         if (ex) rate = wave_mono ? rate_from_keys<kQuant>(keys, recip)
                                  : rate_by_quantizing<kQuant>(D, recip);
         const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
-        s_rate[tid] = (uint8_t)rate;
-        const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
+        const uint32_t rmax = wave_max(rate);
+        s_rate[parity][tid] = (uint8_t)rate;
+        if (lane == 0) s_wmax[parity][wave] = rmax;
+        const TileScan sc = tile_scan(bytes, tid, s_wave[parity]);  // the barrier
+        uint32_t tile_rmax = 0;
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) tile_rmax = max(tile_rmax, s_wmax[parity][w]);
+        const bool wide_tile = tile_rmax > 15u;
         const uint32_t R = g.header_bytes;
         if (tid < kTileBlocks / 4) {
-            const uint32_t word = (uint32_t)s_rate[4 * tid] |
-                                  ((uint32_t)s_rate[4 * tid + 1] << 8) |
-                                  ((uint32_t)s_rate[4 * tid + 2] << 16) |
-                                  ((uint32_t)s_rate[4 * tid + 3] << 24);
-            *to_global(reinterpret_cast<uint32_t*>(cur.J.out + cur.tile * kTileBlocks + 4 * tid)) = word;
+            const uint8_t* r = s_rate[parity];
+            const uint32_t word = (uint32_t)r[4 * tid] | ((uint32_t)r[4 * tid + 1] << 8) |
+                                  ((uint32_t)r[4 * tid + 2] << 16) |
+                                  ((uint32_t)r[4 * tid + 3] << 24);
+            *to_global(reinterpret_cast<uint32_t*>(job_of(p, cur).out + cur.tile * kTileBlocks + 4 * tid)) = word;
         }
         const bool last_tile = cur.tile + 1 == g.tiles_per_job;
         if (last_tile) {
             for (uint32_t off = (cur.tile + 1) * kTileBlocks + 4u * tid; off < R;
                  off += 4u * kThreads)
-                *to_global(reinterpret_cast<uint32_t*>(cur.J.out + off)) = 0u;
+                *to_global(reinterpret_cast<uint32_t*>(job_of(p, cur).out + off)) = 0u;
         }
         if (wave == 0) lookback_publish(p.tile_state, cur.t, cur.tile, sc.total, p.epoch);
-        const uint32_t rmax = wave_max(rate);
+
+        // d. the pending tile's payload out (its prefix came with the scan)
+        if (pending) {
+            const PendingTile& q = s_pend[parity ^ 1u];
+            const uint32_t woff = s_pwave[wave][0], words = s_pwave[wave][1];
+            if (words)
+                copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[parity] + woff),
+                             words, &s_stage[wave][0], lane);
+        }
+
         // Fields (cu:180-231).  signhi: (sign << 15) | |q| rows, whose
         // transpose gives planes 0..14 then the sign word; otherwise
         // ((|q| << 1) | sign) & 0xFFFF rows, whose transpose gives the words
@@ -1273,7 +1351,7 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         if (rmax > 15u) {
             // Rates 16..31 (rare): the high fields (|q| >> 15: planes 15..30,
             // words w_16..w_31) are transposed and parked in the wave's
-            // staging words, which this path does not use for staging.
+            // staging words (free again after d.).
             build_rows_hi_chained<kQuant>(D, recip, P);
             transpose16x2(P);
 #pragma unroll
@@ -1288,25 +1366,8 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
             }
         }
 
-        // d. offset
-        if (wave == 0) {
-            const uint32_t prefix = lookback_wait(p.tile_state, cur.t, cur.tile,
-                                                  sc.total, p.epoch, p.error,
-                                                  p.host_ctl);
-            if (lane == 0) {
-                s_prefix = prefix;
-                if (last_tile)
-                    __hip_atomic_store(&p.host_sizes[cur.job], R + prefix + sc.total,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                if (cur.tile == 0)
-                    __hip_atomic_store(&p.host_bounds[cur.job], eb, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_SYSTEM);
-            }
-        }
-        __syncthreads();
-
         // c. the next tile's keys and min/max (its loads were issued one
-        // iteration ago and complete here, before this tile's stores)
+        // iteration ago and complete here)
         uint32_t nkeys = 0;
         uint32_t nnan = 0;
         if (has_next) {
@@ -1315,38 +1376,78 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
                 publish_tile_keys(p, nxt.t, nkeys >> 16, nkeys & 0xFFFFu, s_min, s_max, tid);
         }
 
-        // e. payload (cu:302-358): sign word, then `rate` plane words
-        if (rmax != 0) {
-            const uint32_t count = rate ? rate + 1u : 0u;
-            uint8_t* base = cur.J.out + R + s_prefix;
-            if (rmax <= 15u) {
-                const uint32_t wave_off = __builtin_amdgcn_readfirstlane(sc.exclusive);
-                uint32_t* wave_dst = reinterpret_cast<uint32_t*>(base + wave_off);
-                const uint32_t g0 = (uint32_t)(reinterpret_cast<uintptr_t>(wave_dst) >> 2);
-                const uint32_t total =
-                    (uint32_t)__builtin_amdgcn_readlane((int)(sc.exclusive + bytes), 63) - wave_off;
-                transpose16x2(P);
-                uint32_t W[16];
-                if (signhi) {
-                    W[0] = P[15];
+        // e. payload (cu:302-358): sign word, then `rate` plane words.
+        // Waves with rates <= 15 stage theirs; it goes out next iteration,
+        // or, in a tile with a wider wave, right after this tile's look-back.
+        const uint32_t count = rate ? rate + 1u : 0u;
+        const uint32_t wave_off = __builtin_amdgcn_readfirstlane(sc.exclusive);
+        const uint32_t wave_words =
+            ((uint32_t)__builtin_amdgcn_readlane((int)(sc.exclusive + bytes), 63) - wave_off) >> 2;
+        if (rmax != 0 && rmax <= 15u) {
+            transpose16x2(P);
+            uint32_t W[16];
+            if (signhi) {
+                W[0] = P[15];
 #pragma unroll
-                    for (int j = 1; j < 16; ++j) W[j] = P[j - 1];
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) W[j] = P[j];
-                }
-                stage_and_store(wave_dst, g0, W, count, (sc.exclusive - wave_off) >> 2,
-                                rmax + 1u, total >> 2, &s_stage[wave][0], lane);
+                for (int j = 1; j < 16; ++j) W[j] = P[j - 1];
             } else {
-                // Rates 16..31 (rare): each lane writes its own words, the
-                // low fields built above, then the parked high fields.
+#pragma unroll
+                for (int j = 0; j < 16; ++j) W[j] = P[j];
+            }
+            stage_payload(W, count, (sc.exclusive - wave_off) >> 2, rmax + 1u,
+                          &s_stage[wave][0]);
+        }
+        if (!wide_tile) {
+            if (lane == 0) {
+                s_pwave[wave][0] = wave_off;
+                s_pwave[wave][1] = wave_words;
+            }
+            if (tid == 0) {
+                PendingTile q;
+                q.t = cur.t;
+                q.tile = cur.tile;
+                q.job = cur.job;
+                q.total = sc.total;
+                q.R = R;
+                q.last = last_tile;
+                q.first = cur.tile == 0;
+                q.eb = eb;
+                q.out = job_of(p, cur).out;
+                s_pend[parity] = q;
+            }
+            pending = true;
+        } else {
+            // This tile's look-back now (wave 0; one more barrier hands the
+            // prefix over).
+            if (wave == 0) {
+                const uint32_t pf = lookback_wait(p.tile_state, cur.t, cur.tile, sc.total,
+                                                  p.epoch, p.error, p.host_ctl);
+                if (lane == 0) {
+                    s_prefix[parity ^ 1u] = pf;
+                    if (last_tile)
+                        __hip_atomic_store(&p.host_sizes[cur.job], R + pf + sc.total,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    if (cur.tile == 0)
+                        __hip_atomic_store(&p.host_bounds[cur.job], eb, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+            }
+            __syncthreads();
+            uint8_t* base = job_of(p, cur).out + R + s_prefix[parity ^ 1u];
+            if (rmax > 15u) {
+                // Rates 16..31 (rare): each lane writes its own words, the low
+                // fields, then the parked high fields.
                 uint32_t* dst = reinterpret_cast<uint32_t*>(base + sc.exclusive);
                 transpose16x2(P);
                 store_words<16>(dst, P, count < 16u ? count : 16u, 16u);
 #pragma unroll
                 for (int j = 0; j < 16; ++j) P[j] = s_stage[wave][64 * j + lane];
                 store_words<16>(dst + 16, P, count > 16u ? count - 16u : 0u, rmax - 15u);
+            } else if (wave_words) {
+                copy_payload(reinterpret_cast<uint32_t*>(base + wave_off), wave_words,
+                             &s_stage[wave][0], lane);
             }
+            pending = false;
         }
 
         // f. advance
@@ -1359,8 +1460,34 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         has_next = cur.t + G < p.total_tiles;
         if (has_next) {
             nxt = tile_ctx(p, cur.t + G, s_gfirst);
-            load_block_regs(nxt, p.groups[nxt.gi], wave, lane, N, &bad);
+            load_block_regs(p, nxt, p.groups[nxt.gi], wave, lane, N, &bad);
         }
+    }
+    // The last staged payload.
+    if (pending) {
+        const int tid = loop_tid();
+        const int lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        if (wave == 0) {
+            const PendingTile& q = s_pend[parity];
+            const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
+                                              p.epoch, p.error, p.host_ctl);
+            if (lane == 0) {
+                s_prefix[2] = pf;
+                if (q.last)
+                    __hip_atomic_store(&p.host_sizes[q.job], q.R + pf + q.total,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (q.first)
+                    __hip_atomic_store(&p.host_bounds[q.job], q.eb, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+        __syncthreads();
+        const PendingTile& q = s_pend[parity];
+        const uint32_t woff = s_pwave[wave][0], words = s_pwave[wave][1];
+        if (words)
+            copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[2] + woff),
+                         words, &s_stage[wave][0], lane);
     }
     if (bad & 1) flag_error(p.error, p.host_ctl, kErrLayerIndex);
 }
