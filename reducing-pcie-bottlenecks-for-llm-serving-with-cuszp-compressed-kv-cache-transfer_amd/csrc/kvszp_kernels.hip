@@ -462,9 +462,19 @@ __device__ __forceinline__ void lookback_publish(unsigned long long* state,
 // back over earlier tiles of the job 64 at a time until it meets one whose
 // inclusive prefix is published, publishes this tile's inclusive prefix and
 // returns the exclusive one (bytes of earlier tiles of the job).
+// lookback_first: the first window's words (what lookback_wait reads first),
+// for a caller that issues that read early to overlap it with other waits.
+__device__ __forceinline__ unsigned long long lookback_first(
+    const unsigned long long* state, uint32_t t, uint32_t tile) {
+    const uint32_t lane = __lane_id();
+    return (tile != 0 && lane < (tile < 64u ? tile : 64u)) ? load_relaxed(&state[t - 1 - lane])
+                                                          : 0ull;
+}
+
 __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
                                   uint32_t tile, uint32_t total, uint32_t epoch,
-                                  uint32_t* err, uint32_t* host_ctl) {
+                                  uint32_t* err, uint32_t* host_ctl,
+                                  bool have_first = false, unsigned long long first = 0) {
     if (tile == 0) return 0;
     const int lane = __lane_id();
     const uint32_t tag_agg = epoch * 4u + 1u;
@@ -479,7 +489,12 @@ __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
             nwin == 64u ? ~0ull : ((1ull << nwin) - 1ull);
         unsigned long long w = 0, need = 0, incl = 0;
         for (uint32_t spins = 0;; ++spins) {
-            w = in_win ? load_relaxed(&state[pos - lane]) : 0ull;
+            if (have_first) {  // the caller's early read of this window
+                w = first;
+                have_first = false;
+            } else {
+                w = in_win ? load_relaxed(&state[pos - lane]) : 0ull;
+            }
             const uint32_t tag = (uint32_t)(w >> 32);
             incl = __ballot(in_win && tag == tag_inc);
             const unsigned long long ready =
@@ -977,12 +992,67 @@ __device__ __forceinline__ uint64_t enc_block_source(const Group& g, uint32_t ti
 }
 
 // This thread's block (zeros when it does not exist): four 16-byte loads.
+// A layer index outside [0, source_layers) is reported at once (the block is
+// then read from layer 0).
 __device__ __forceinline__ void load_block_regs(const CompressParams& p, const TileCtx& c,
                                                 const Group& g, int wave, int lane,
-                                                uint32_t* d, uint32_t* bad) {
+                                                uint32_t* d) {
     const bool ex = block_exists(g, c.tile, wave * 64 + lane);
+    uint32_t bad = 0;
     const g_u32x4* src = (const g_u32x4*)to_global(
-        job_of(p, c).in + (ex ? enc_block_source(g, c.tile, wave, lane, bad) : 0));
+        job_of(p, c).in + (ex ? enc_block_source(g, c.tile, wave, lane, &bad) : 0));
+    if (bad) flag_error(p.error, p.host_ctl, kErrLayerIndex);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u32x4 v = ex ? src[i] : u32x4{0u, 0u, 0u, 0u};
+        d[4 * i + 0] = v.x;
+        d[4 * i + 1] = v.y;
+        d[4 * i + 2] = v.z;
+        d[4 * i + 3] = v.w;
+    }
+}
+
+// Source of a tile's blocks for one wave, worked out ahead of the loads: when
+// the wave's 64 blocks are consecutive in memory, `base` is its first block
+// (wave-uniform) and lane l reads base + 32 l; otherwise base is null and
+// each lane maps its own block when loading.
+struct WaveSource {
+    const uint16_t* base;
+};
+
+__device__ __forceinline__ WaveSource wave_source(const CompressParams& p, const TileCtx& c,
+                                                  const Group& g, int wave) {
+    constexpr uint32_t kRun = 64u * kBlockElems;
+    WaveSource s;
+    const uint16_t* in = job_of(p, c).in;
+    const uint32_t E = c.tile * (uint32_t)kTileElems + (uint32_t)wave * kRun;
+    if (g.layers == nullptr) {
+        s.base = in + E;
+        return s;
+    }
+    const uint32_t epl = (uint32_t)g.elements_per_layer;
+    const uint32_t per_prefix = (uint32_t)g.selected_layers * epl;
+    const uint32_t pre = E / per_prefix;
+    const uint32_t within = E - pre * per_prefix;
+    const uint32_t layer = within / epl;
+    const uint32_t inner = within - layer * epl;
+    const int64_t l = load_const(g.layers, layer);
+    s.base = (inner + kRun <= epl && l >= 0 && (uint64_t)l < g.source_layers)
+                 ? in + ((uint64_t)pre * g.source_layers + (uint64_t)l) * epl + inner
+                 : nullptr;
+    return s;
+}
+
+// This thread's block from a WaveSource (zeros when it does not exist).
+__device__ __forceinline__ void load_block_from(const CompressParams& p, const TileCtx& c,
+                                                const Group& g, WaveSource s, int wave,
+                                                int lane, uint32_t* d) {
+    if (s.base == nullptr) {
+        load_block_regs(p, c, g, wave, lane, d);
+        return;
+    }
+    const bool ex = block_exists(g, c.tile, wave * 64 + lane);
+    const g_u32x4* src = (const g_u32x4*)to_global(s.base + (ex ? (uint32_t)lane * kBlockElems : 0u));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const u32x4 v = ex ? src[i] : u32x4{0u, 0u, 0u, 0u};
@@ -995,12 +1065,31 @@ __device__ __forceinline__ void load_block_regs(const CompressParams& p, const T
 
 // Block keys packed as (min key << 16) | max key, plus whether the block
 // holds a NaN (fminf/fmaxf skip NaN, cu:78-79; the quantizer does not).
+//
+// Fast case on the raw BF16 patterns: read as signed 16-bit numbers, the
+// patterns with the sign bit clear order by value and lie above all others;
+// read as unsigned numbers, the patterns with the sign bit set lie above all
+// others and order by magnitude.  So in a block holding both kinds, the
+// signed maximum is its largest value and the unsigned maximum its smallest
+// (two packed operations per pair of values).  NaN patterns exceed every
+// other pattern of their sign (0x7F81.. and 0xFF81..) and are caught by the
+// range checks; blocks of one sign, or with a NaN, take the general path.
 __device__ __forceinline__ uint32_t block_keys(const uint32_t* d, bool exists,
                                                uint32_t& nan) {
     nan = 0;
     if (!exists) return (kKeyEmptyMin << 16) | kKeyEmptyMax;
-    u16x2 mn = {0xFFFFu, 0xFFFFu}, mx = {0u, 0u};
+    s16x2 smax = {(short)-32768, (short)-32768};
+    u16x2 umax = {0u, 0u};
 #pragma unroll
+    for (int i = 0; i < kBlockElems / 2; ++i) {
+        smax = __builtin_elementwise_max(smax, __builtin_bit_cast(s16x2, d[i]));
+        umax = __builtin_elementwise_max(umax, __builtin_bit_cast(u16x2, d[i]));
+    }
+    const int32_t hs = smax.x > smax.y ? smax.x : smax.y;
+    const uint32_t hu = umax.x > umax.y ? umax.x : umax.y;
+    if (hs >= 0 && hs <= 0x7F80 && hu >= 0x8000u && hu <= 0xFF80u)
+        return ((~hu & 0xFFFFu) << 16) | ((uint32_t)hs | 0x8000u);
+    u16x2 mn = {0xFFFFu, 0xFFFFu}, mx = {0u, 0u};
     for (int i = 0; i < kBlockElems / 2; ++i) {
         // key = sign ? ~h : h | 0x8000, for both halves at once
         const uint32_t neg = __builtin_bit_cast(
@@ -1089,6 +1178,10 @@ __device__ __forceinline__ void exchange_minmax(const CompressParams& p,
     }
 }
 
+// Keys of -inf (min) and +inf (max): every |x * recip| is infinite, so the
+// block counts as outside the monotone range.
+constexpr uint32_t kNanRateKeys = (0x007Fu << 16) | 0xFF80u;
+
 // Rate of a block from its keys (see b. above; the caller checked that no
 // |x * recip| of the block reaches 2^30 and that it holds no NaN).
 template <int kQuant>
@@ -1150,11 +1243,14 @@ __device__ __forceinline__ void build_rows_signhi(uint32_t* d, float recip, uint
 }
 
 // A wave's payload staged in LDS: lane l's block is words [off, off + count)
-// of the wave's payload, W[0..count) its stream words.  Words are written
-// from the highest index down: a lane's unused slots (index >= count) only
-// ever fall on later lanes' words, which are written afterwards, or past the
-// payload end, so `stage` needs room for 1024 + 16 words.
-__device__ __forceinline__ void stage_payload(const uint32_t* W, uint32_t count,
+// of the wave's payload.  The stream words are the transposed rows P:
+// w_j = P[j] (kSignHi false), or w_0 = P[15] and w_j = P[j - 1] (sign-high
+// rows).  Words are written from the highest index down: a lane's unused
+// slots (index >= count) only ever fall on later lanes' words, which are
+// written afterwards, or past the payload end, so `stage` needs room for
+// 1024 + 16 words.
+template <bool kSignHi>
+__device__ __forceinline__ void stage_payload(const uint32_t* P, uint32_t count,
                                               uint32_t off, uint32_t cmax,
                                               uint32_t* stage) {
     __asm__ volatile("" ::: "memory");
@@ -1162,38 +1258,20 @@ __device__ __forceinline__ void stage_payload(const uint32_t* W, uint32_t count,
         uint32_t* s = stage + off;
 #pragma unroll
         for (int j = 15; j >= 0; --j)
-            if ((uint32_t)j < cmax) s[j] = W[j];
+            if ((uint32_t)j < cmax) s[j] = kSignHi ? P[(j + 15) & 15] : P[j];
     }
     __asm__ volatile("" ::: "memory");
 }
 
-// Writes a wave's staged payload (`words` words) to `dst` (4-byte aligned)
-// with 16-byte stores on 16-byte boundaries: destination group q covers
-// dst[4q - shift .. 4q - shift + 4), shift = (dst / 4) mod 4, i.e. staged
-// words 4q - shift .. ; partial groups at either end are written word by
-// word.
+// Writes a wave's staged payload (`words` words) to `dst` (4-byte aligned):
+// word w goes out from lane w mod 64, so every store covers 256 contiguous
+// bytes and every LDS read 64 consecutive words (no bank conflicts).
 __device__ __forceinline__ void copy_payload(uint32_t* dst, uint32_t words,
                                              const uint32_t* stage, int lane) {
     __builtin_amdgcn_wave_barrier();
     __asm__ volatile("" ::: "memory");
-    const uint32_t shift = (uint32_t)(reinterpret_cast<uintptr_t>(dst) >> 2) & 3u;
-    g_u32* d = to_global(dst - shift);
-    const uint32_t groups = (shift + words + 3u) >> 2;
-    for (uint32_t q = (uint32_t)lane; q < groups; q += 64u) {
-        const int32_t lo = (int32_t)(4u * q) - (int32_t)shift;  // staged index of d[4q]
-        if (lo >= 0 && lo + 4 <= (int32_t)words) {
-            u32x4 v;
-            v.x = stage[lo + 0];
-            v.y = stage[lo + 1];
-            v.z = stage[lo + 2];
-            v.w = stage[lo + 3];
-            *(g_u32x4*)(d + 4u * q) = v;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (lo + i >= 0 && lo + i < (int32_t)words) d[4u * q + i] = stage[lo + i];
-        }
-    }
+    g_u32* d = to_global(dst);
+    for (uint32_t w = (uint32_t)lane; w < words; w += 64u) d[w] = stage[w];
     __builtin_amdgcn_wave_barrier();
     __asm__ volatile("" ::: "memory");  // before the words are reused
 }
@@ -1244,27 +1322,30 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
     __syncthreads();
     const uint32_t G = gridDim.x;
     const bool fused = p.bound_mode == kBoundFused;
-    uint32_t bad = 0;
     bool pending = false;  // a tile's payload waits in the staging words
 
     // Prologue: the first tile and its keys (published), the next one loading.
     TileCtx cur = tile_ctx(p, blockIdx.x, s_gfirst);
     uint32_t D[16], N[16];
+    // Rate keys of the current tile's blocks: the published keys, except
+    // that a block holding a NaN keeps the keys of -inf and +inf, which
+    // sends its wave down the exact path in b.
     uint32_t keys;
-    uint32_t nan;  // 0/1 per lane (a VGPR rather than a lane mask)
     bool has_next;
     TileCtx nxt;
     {
         const int tid = loop_tid();
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const Group& g = p.groups[cur.gi];
-        load_block_regs(p, cur, g, wave, tid & 63, D, &bad);
+        load_block_regs(p, cur, g, wave, tid & 63, D);
+        uint32_t nan;
         keys = block_keys(D, block_exists(g, cur.tile, tid), nan);
         if (fused) publish_tile_keys(p, cur.t, keys >> 16, keys & 0xFFFFu, s_min, s_max, tid);
+        if (nan) keys = kNanRateKeys;
         has_next = cur.t + G < p.total_tiles;
         if (has_next) {
             nxt = tile_ctx(p, cur.t + G, s_gfirst);
-            load_block_regs(p, nxt, p.groups[nxt.gi], wave, tid & 63, N, &bad);
+            load_block_regs(p, nxt, p.groups[nxt.gi], wave, tid & 63, N);
         }
     }
 
@@ -1276,7 +1357,24 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         const Group& g = p.groups[cur.gi];
         const bool ex = block_exists(g, cur.tile, tid);
 
-        // a. bound; wave 0 also finishes the pending tile's look-back
+        // The tile loaded at c. (two ahead): its context and this wave's
+        // source now, so that the scalar loads and divisions overlap the
+        // exchange below.
+        const bool has_after = has_next && nxt.t + G < p.total_tiles;
+        TileCtx after = nxt;
+        WaveSource asrc{nullptr};
+        if (has_after) {
+            after = tile_ctx(p, nxt.t + G, s_gfirst);
+            asrc = wave_source(p, after, p.groups[after.gi], wave);
+        }
+
+        // a. bound; wave 0 also finishes the pending tile's look-back (its
+        // first read issued before the exchange's, so the two overlap)
+        unsigned long long lb_first = 0;
+        if (pending && wave == 0) {
+            const PendingTile& q = s_pend[parity ^ 1u];
+            lb_first = lookback_first(p.tile_state, q.t, q.tile);
+        }
         float eb = job_of(p, cur).eps;
         if (fused) {
             uint32_t kmin, kmax;
@@ -1288,7 +1386,8 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         if (pending && wave == 0) {
             const PendingTile& q = s_pend[parity ^ 1u];
             const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                              p.epoch, p.error, p.host_ctl);
+                                              p.epoch, p.error, p.host_ctl, true,
+                                              lb_first);
             if (lane == 0) {
                 s_prefix[parity] = pf;
                 if (q.last)
@@ -1303,7 +1402,7 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         // b. rates, tile scan, header bytes (padding zeroed by the last
         // tile), aggregate out
         const float bmax = fmaxf(fabsf(key_value(keys >> 16)), fabsf(key_value(keys & 0xFFFFu)));
-        const bool mono = !ex || (nan == 0 && fabsf(bmax * recip) < 0x1p30f);
+        const bool mono = !ex || fabsf(bmax * recip) < 0x1p30f;
         const bool wave_mono = __ballot(!mono) == 0ull;  // wave-uniform
         uint32_t rate = 0;
         if (ex) rate = wave_mono ? rate_from_keys<kQuant>(keys, recip)
@@ -1367,13 +1466,19 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         }
 
         // c. the next tile's keys and min/max (its loads were issued one
-        // iteration ago and complete here)
+        // iteration ago and complete here); this tile's values are no longer
+        // needed, so the next tile moves into D and the one after it starts
+        // loading into N -- each load then has a whole iteration to arrive.
         uint32_t nkeys = 0;
-        uint32_t nnan = 0;
         if (has_next) {
+            uint32_t nnan;
             nkeys = block_keys(N, block_exists(p.groups[nxt.gi], nxt.tile, tid), nnan);
             if (fused)
                 publish_tile_keys(p, nxt.t, nkeys >> 16, nkeys & 0xFFFFu, s_min, s_max, tid);
+            if (nnan) nkeys = kNanRateKeys;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) D[i] = N[i];
+            if (has_after) load_block_from(p, after, p.groups[after.gi], asrc, wave, lane, N);
         }
 
         // e. payload (cu:302-358): sign word, then `rate` plane words.
@@ -1385,17 +1490,11 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
             ((uint32_t)__builtin_amdgcn_readlane((int)(sc.exclusive + bytes), 63) - wave_off) >> 2;
         if (rmax != 0 && rmax <= 15u) {
             transpose16x2(P);
-            uint32_t W[16];
-            if (signhi) {
-                W[0] = P[15];
-#pragma unroll
-                for (int j = 1; j < 16; ++j) W[j] = P[j - 1];
-            } else {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) W[j] = P[j];
-            }
-            stage_payload(W, count, (sc.exclusive - wave_off) >> 2, rmax + 1u,
-                          &s_stage[wave][0]);
+            const uint32_t off = (sc.exclusive - wave_off) >> 2;
+            if (signhi)
+                stage_payload<true>(P, count, off, rmax + 1u, &s_stage[wave][0]);
+            else
+                stage_payload<false>(P, count, off, rmax + 1u, &s_stage[wave][0]);
         }
         if (!wide_tile) {
             if (lane == 0) {
@@ -1453,15 +1552,9 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         // f. advance
         if (!has_next) break;
         cur = nxt;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) D[i] = N[i];
         keys = nkeys;
-        nan = nnan;
         has_next = cur.t + G < p.total_tiles;
-        if (has_next) {
-            nxt = tile_ctx(p, cur.t + G, s_gfirst);
-            load_block_regs(p, nxt, p.groups[nxt.gi], wave, lane, N, &bad);
-        }
+        if (has_next) nxt = tile_ctx(p, cur.t + G, s_gfirst);
     }
     // The last staged payload.
     if (pending) {
@@ -1489,7 +1582,6 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
             copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[2] + woff),
                          words, &s_stage[wave][0], lane);
     }
-    if (bad & 1) flag_error(p.error, p.host_ctl, kErrLayerIndex);
 }
 
 // ---- relative-bound pre-pass (jobs too long for the fused exchange) -------
