@@ -11,8 +11,11 @@ does for this job (vllm_v1_compressed_offload.py:1286-1569 and 1815-2006):
 
   store   : one compress_batch_fixed_bf16_indexed_groups call over all 512
             (page, segment) requests (blocking: sizes come back to the host)
-  restore : one decompress_batch_fixed_bf16_indexed_scatter call per group,
-            writing straight into fresh KV pages
+  restore : the reference's one decompress_batch_fixed_bf16_indexed_scatter
+            call per group, writing straight into fresh KV pages -- by
+            default as ONE decompress_batch_fixed_bf16_indexed_scatter_groups
+            launch over both groups (same output; --restore-per-group runs
+            the per-group calls instead)
 
 Calls go through the C ABI (libkvszp.so) with the page-pointer arrays built
 once, inputs resident in HBM.  `value` = uncompressed BF16 bytes of the KV
@@ -47,7 +50,8 @@ def log(msg: str) -> None:
 class Workload:
     """Config 1 pages, compressed slabs and pointer tables, built once."""
 
-    def __init__(self, seed: int, tokens: int | None = None):
+    def __init__(self, seed: int, tokens: int | None = None,
+                 grouped_restore: bool = True):
         import torch
 
         import kv_synth
@@ -100,6 +104,11 @@ class Workload:
             self.group_slices.append((start, start + self.num_pages))
             start += self.num_pages
         # Per-group restore arguments, built once like the other tables.
+        self.grouped_restore = grouped_restore
+        self.stream_table = kvszp.ptr_array(self.stream_ptrs)
+        # one destination page per request: every group restores into the
+        # same fresh pages
+        self.dest_table = kvszp.ptr_array(dest_ptrs * len(self.groups))
         self.restore_args = []
         for g, (lo, hi) in enumerate(self.group_slices):
             cnt = hi - lo
@@ -118,6 +127,13 @@ class Workload:
 
     def restore(self) -> None:
         k = self.kvszp
+        if self.grouped_restore:
+            k.check(self.ctx.decompress_indexed_scatter_groups(
+                self.stream_table, self.sizes, self.bounds, self.batch,
+                self.dest_table, self.idx_ptrs, self.sel, self.group_sizes,
+                len(self.groups), 2, self.shape.layers, self.epl,
+                self.stream))
+            return
         for comp, sizes, bounds, cnt, idx, sel in self.restore_args:
             k.check(self.ctx.decompress_indexed_scatter(
                 comp, sizes, bounds, cnt, self.dest_ptrs, idx, sel, 2,
@@ -267,6 +283,10 @@ def main() -> int:
     ap.add_argument("--cpu-pages", type=int, default=256,
                     help="pages of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--restore-per-group", action="store_true",
+                    help="restore with one indexed_scatter call per layer "
+                         "group (the reference's call pattern) instead of "
+                         "one grouped launch")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference "
                          "kernel for scaling rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -296,7 +316,7 @@ def main() -> int:
                           "copies": 3}), flush=True)
         return 0
     log("building workload")
-    w = Workload(args.seed)
+    w = Workload(args.seed, grouped_restore=not args.restore_per_group)
     log(f"workload: {w.num_pages} pages x {w.page_numel} BF16, "
         f"{w.batch} segment requests")
     for _ in range(max(1, args.warmup)):
@@ -329,7 +349,9 @@ def main() -> int:
         w.step()
     torch.cuda.synchronize()
     w.ctx.enable_timing(0)
-    kt["decompress_ms"] = w.ctx.drain_timing()["decompress_ms"]
+    dt = w.ctx.drain_timing()
+    kt["decompress_ms"] = dt["decompress_ms"]
+    dec_launches = max(1, dt["decompress_launches"] // max(1, args.steps))
 
     # Algorithmic bytes per launch: compress reads 2N and writes S per
     # segment; restore reads S and writes 2N.
@@ -344,7 +366,8 @@ def main() -> int:
     if comp_ms >= dec_ms_step:
         dom = ("compress_kernel", comp_hbm, comp_launch_bytes)
     else:
-        dom = ("decompress_kernel", dec_hbm, (w.bf16_bytes + s_bytes) / len(w.groups))
+        dom = ("decompress_kernel", dec_hbm,
+               (w.bf16_bytes + s_bytes) / dec_launches)
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -367,7 +390,8 @@ def main() -> int:
             "workload": "qwen2.5-1.5b 4k store+restore (configs[1]): 256 pages "
                         "x [2,28,16,2,128] bf16, layers {0,1,2,5,19,20,21} REL "
                         "1e-5 + 21 layers REL 1e-4, indexed_groups compress + "
-                        "2x indexed_scatter restore",
+                        + ("2x indexed_scatter restore" if args.restore_per_group
+                           else "indexed_scatter_groups restore"),
             "pages": w.num_pages,
             "page_elements": w.page_numel,
             "segment_requests": w.batch,

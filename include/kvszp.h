@@ -157,6 +157,21 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter(
     size_t prefix_count, size_t source_layers, size_t elements_per_layer,
     kvszp_stream_t stream);
 
+/* Several calls of kvszp_decompress_batch_fixed_bf16_indexed_scatter in
+ * ONE kernel launch: requests are laid out group by group like
+ * kvszp_compress_batch_fixed_bf16_indexed_groups (group g covers the next
+ * group_sizes[g] entries and uses layer_indices[g], selected_layers[g] long).
+ * No reference counterpart: the reference decodes a mixed-bound job with one
+ * decompress_batch_fixed_bf16_indexed_scatter call per layer group
+ * (vllm_v1_compressed_offload.py:1815-2006); this entry point gives that
+ * caller the same result in a single launch. */
+int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups(
+    kvszp_ctx* ctx, const void* const* compressed, const uint64_t* sizes,
+    const float* error_bounds, size_t batch, void* const* destinations,
+    const int64_t* const* layer_indices, const size_t* selected_layers,
+    const size_t* group_sizes, size_t num_groups, size_t prefix_count,
+    size_t source_layers, size_t elements_per_layer, kvszp_stream_t stream);
+
 /* Waits for `stream` and reports any error a kernel of this context flagged
  * since the last check (decompress calls only enqueue, so their device-side
  * errors surface here or at the next compress call).  No reference

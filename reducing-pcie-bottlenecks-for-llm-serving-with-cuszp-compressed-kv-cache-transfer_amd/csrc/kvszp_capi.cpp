@@ -490,40 +490,62 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     return KVSZP_OK;
 }
 
-// Common decompress path.
+// Common decompress path: `specs` are the groups, requests laid out group by
+// group (one launch for all of them).
 int decompress_groups(kvszp_ctx* c, const void* const* compressed,
                       const uint64_t* sizes, const float* bounds, size_t batch,
-                      const GroupSpec& spec, int dst_kind,
+                      const std::vector<GroupSpec>& specs, int dst_kind,
                       const std::vector<uint16_t*>& dst_base,
                       const std::vector<uint16_t*>& dest_table, uint64_t dpp,
                       uint64_t epd, bool aligned16, hipStream_t stream) {
     int rc = use_device(c);
     if (rc) return rc;
-    if (spec.n == 0 || spec.n > kMaxElements)
-        return fail(KVSZP_EINVAL, "segment of %llu elements unsupported",
-                    (unsigned long long)spec.n);
-    const uint32_t R = header_bytes_of(spec.n);
+    if (specs.empty() || specs.size() > (size_t)kMaxGroups)
+        return fail(KVSZP_EINVAL, "between 1 and %d groups supported", kMaxGroups);
+    DecompressParams p;
+    std::memset(&p, 0, sizeof(p));
     std::vector<DecompressJob> jobs(batch);
-    for (size_t i = 0; i < batch; ++i) {
-        const uintptr_t in = (uintptr_t)compressed[i];
-        // cuszp_wrapper.cpp:1077: a zero size is rejected.  A stream shorter
-        // than its own header cannot be decoded either.
-        if (!in || sizes[i] == 0)
-            return fail(KVSZP_EINVAL, "invalid compressed page %zu", i);
-        if (sizes[i] < R)
-            return fail(KVSZP_EINVAL, "stream %zu (%llu bytes) shorter than its "
-                        "%u-byte header", i, (unsigned long long)sizes[i], R);
-        if (sizes[i] > 0xFFFFFFFFull)
-            return fail(KVSZP_EINVAL, "stream %zu too large", i);
-        if (in & 3u)
-            return fail(KVSZP_EINVAL, "compressed buffer %zu not 4-byte aligned", i);
-        jobs[i].in = reinterpret_cast<const uint8_t*>(in);
-        jobs[i].dst = dst_kind == kDstMulti ? nullptr : dst_base[i];
-        jobs[i].eb = bounds[i];
-        jobs[i].size = (uint32_t)sizes[i];
+    uint64_t total_tiles = 0;
+    size_t job = 0;
+    for (size_t gi = 0; gi < specs.size(); ++gi) {
+        const GroupSpec& spec = specs[gi];
+        if (spec.n == 0 || spec.n > kMaxElements)
+            return fail(KVSZP_EINVAL, "segment of %llu elements unsupported",
+                        (unsigned long long)spec.n);
+        const uint32_t R = header_bytes_of(spec.n);
+        Group& g = p.groups[gi];
+        g.n = spec.n;
+        g.layers = spec.layers;
+        g.selected_layers = spec.sel;
+        g.source_layers = spec.src;
+        g.elements_per_layer = spec.epl;
+        g.first_job = (uint32_t)job;
+        g.first_tile = (uint32_t)total_tiles;
+        g.tiles_per_job = (uint32_t)((spec.n + kTileElems - 1) / kTileElems);
+        g.header_bytes = R;
+        total_tiles += (uint64_t)g.tiles_per_job * spec.jobs;
+        for (uint32_t k = 0; k < spec.jobs; ++k, ++job) {
+            if (job >= batch) return fail(KVSZP_EINVAL, "group sizes exceed batch");
+            const size_t i = job;
+            const uintptr_t in = (uintptr_t)compressed[i];
+            // cuszp_wrapper.cpp:1077: a zero size is rejected.  A stream shorter
+            // than its own header cannot be decoded either.
+            if (!in || sizes[i] == 0)
+                return fail(KVSZP_EINVAL, "invalid compressed page %zu", i);
+            if (sizes[i] < R)
+                return fail(KVSZP_EINVAL, "stream %zu (%llu bytes) shorter than its "
+                            "%u-byte header", i, (unsigned long long)sizes[i], R);
+            if (sizes[i] > 0xFFFFFFFFull)
+                return fail(KVSZP_EINVAL, "stream %zu too large", i);
+            if (in & 3u)
+                return fail(KVSZP_EINVAL, "compressed buffer %zu not 4-byte aligned", i);
+            jobs[i].in = reinterpret_cast<const uint8_t*>(in);
+            jobs[i].dst = dst_kind == kDstMulti ? nullptr : dst_base[i];
+            jobs[i].eb = bounds[i];
+            jobs[i].size = (uint32_t)sizes[i];
+        }
     }
-    const uint32_t tiles_per_job = (uint32_t)((spec.n + kTileElems - 1) / kTileElems);
-    const uint64_t total_tiles = (uint64_t)tiles_per_job * batch;
+    if (job != batch) return fail(KVSZP_EINVAL, "group sizes do not cover the batch");
     if (total_tiles > kMaxTiles) return fail(KVSZP_EINVAL, "batch too large for one launch");
 
     // Packed table: jobs, then (kDstMulti) the destination pointers.
@@ -539,8 +561,6 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     uint32_t epoch;
     if ((rc = next_epoch(c, stream, &epoch))) return rc;
 
-    DecompressParams p;
-    std::memset(&p, 0, sizeof(p));
     p.jobs = reinterpret_cast<const DecompressJob*>(c->tables.ptr);
     p.dests = reinterpret_cast<uint16_t* const*>(
         reinterpret_cast<char*>(c->tables.ptr) + jobs_bytes);
@@ -552,22 +572,12 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     p.ticket_base = c->ticket_next;
     p.epoch = epoch;
     p.total_tiles = (uint32_t)total_tiles;
-    p.num_groups = 1;
+    p.num_groups = (int)specs.size();
     p.dst_kind = dst_kind;
     p.rate0_zero = c->rate0 == KVSZP_RATE0_ZERO ? 1 : 0;
     p.aligned16 = aligned16 ? 1 : 0;
     p.dests_per_page = dpp;
     p.elements_per_dest = epd;
-    Group& g = p.groups[0];
-    g.n = spec.n;
-    g.layers = spec.layers;
-    g.selected_layers = spec.sel;
-    g.source_layers = spec.src;
-    g.elements_per_layer = spec.epl;
-    g.first_job = 0;
-    g.first_tile = 0;
-    g.tiles_per_job = tiles_per_job;
-    g.header_bytes = R;
     const int rec = timing_begin(c, KVSZP_KERNEL_DECOMPRESS);
     hipError_t e;
     if (c->decompress_grid != 0) {
@@ -780,7 +790,8 @@ int kvszp_decompress_batch_fixed_bf16(kvszp_ctx* c, const void* const* compresse
         base[i] = reinterpret_cast<uint16_t*>(output) + i * num_elements_per_page;
     const bool aligned16 =
         ((uintptr_t)output & 15u) == 0 && (num_elements_per_page % 8) == 0;
-    GroupSpec spec{num_elements_per_page, nullptr, 0, 0, 0, (uint32_t)batch};
+    const std::vector<GroupSpec> spec{
+        GroupSpec{num_elements_per_page, nullptr, 0, 0, 0, (uint32_t)batch}};
     return decompress_groups(c, compressed, sizes, error_bounds, batch, spec,
                              kDstLinear, base, {}, 0, 0, aligned16,
                              (hipStream_t)stream);
@@ -810,7 +821,8 @@ int kvszp_decompress_batch_fixed_bf16_scatter(
         if (d & 15u) aligned16 = false;
         dests[i] = reinterpret_cast<uint16_t*>(d);
     }
-    GroupSpec spec{num_elements_per_page, nullptr, 0, 0, 0, (uint32_t)batch};
+    const std::vector<GroupSpec> spec{
+        GroupSpec{num_elements_per_page, nullptr, 0, 0, 0, (uint32_t)batch}};
     if (destinations_per_page == 1) {
         // One destination per page: straight 16-byte stores into the page
         // (cu:383-386, 566-576).
@@ -845,10 +857,54 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter(
             return fail(KVSZP_EINVAL, "invalid BF16 destination page %zu", i);
         dests[i] = reinterpret_cast<uint16_t*>(d);
     }
-    GroupSpec spec{(uint64_t)prefix_count * selected_layers * elements_per_layer,
-                   layer_indices, selected_layers, source_layers,
-                   elements_per_layer, (uint32_t)batch};
+    const std::vector<GroupSpec> spec{
+        GroupSpec{(uint64_t)prefix_count * selected_layers * elements_per_layer,
+                  layer_indices, selected_layers, source_layers, elements_per_layer,
+                  (uint32_t)batch}};
     return decompress_groups(c, compressed, sizes, error_bounds, batch, spec,
+                             kDstIndexed, dests, {}, 0, 0, false,
+                             (hipStream_t)stream);
+}
+
+int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups(
+    kvszp_ctx* c, const void* const* compressed, const uint64_t* sizes,
+    const float* error_bounds, size_t batch, void* const* destinations,
+    const int64_t* const* layer_indices, const size_t* selected_layers,
+    const size_t* group_sizes, size_t num_groups, size_t prefix_count,
+    size_t source_layers, size_t elements_per_layer, kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (batch == 0) return KVSZP_OK;
+    int rc = check_fixed_config(c);
+    if (rc) return rc;
+    if (!compressed || !sizes || !error_bounds || !destinations)
+        return fail(KVSZP_EINVAL, "null pointer argument");
+    if (num_groups == 0 || !layer_indices || !selected_layers || !group_sizes)
+        return fail(KVSZP_EINVAL, "empty group list");
+    std::vector<GroupSpec> specs;
+    uint64_t covered = 0;
+    for (size_t gi = 0; gi < num_groups; ++gi) {
+        if (group_sizes[gi] == 0)
+            return fail(KVSZP_EINVAL, "group %zu is empty", gi);
+        rc = validate_layers(layer_indices[gi], selected_layers[gi], prefix_count,
+                             source_layers, elements_per_layer);
+        if (rc) return rc;
+        specs.push_back(GroupSpec{
+            (uint64_t)prefix_count * selected_layers[gi] * elements_per_layer,
+            layer_indices[gi], selected_layers[gi], source_layers,
+            elements_per_layer, (uint32_t)group_sizes[gi]});
+        covered += group_sizes[gi];
+    }
+    if (covered != batch)
+        return fail(KVSZP_EINVAL, "group sizes sum to %llu, batch is %zu",
+                    (unsigned long long)covered, batch);
+    std::vector<uint16_t*> dests(batch);
+    for (size_t i = 0; i < batch; ++i) {
+        const uintptr_t d = (uintptr_t)destinations[i];
+        if (!d || (d & 1u))
+            return fail(KVSZP_EINVAL, "invalid BF16 destination page %zu", i);
+        dests[i] = reinterpret_cast<uint16_t*>(d);
+    }
+    return decompress_groups(c, compressed, sizes, error_bounds, batch, specs,
                              kDstIndexed, dests, {}, 0, 0, false,
                              (hipStream_t)stream);
 }

@@ -446,6 +446,53 @@ class CuSZpWrapper:
             return False
         return True
 
+    def decompress_batch_fixed_bf16_indexed_scatter_groups(
+            self, compressed_buffers, compressed_sizes, output_tensors,
+            layer_indices, group_sizes, prefix_count, source_layers,
+            elements_per_layer, actual_error_bounds):
+        """Several decompress_batch_fixed_bf16_indexed_scatter calls (one per
+        layer group, vllm_v1_compressed_offload.py:1815-2006) in one launch.
+        Requests are laid out group by group: group g covers the next
+        group_sizes[g] entries and scatters through layer_indices[g].  No
+        reference counterpart; same argument checks and result as the
+        per-group calls."""
+        batch = len(compressed_buffers)
+        if batch == 0:
+            return True
+        if (len(compressed_sizes) != batch or len(actual_error_bounds) != batch
+                or len(output_tensors) != batch or not layer_indices
+                or len(layer_indices) != len(group_sizes)
+                or prefix_count == 0 or source_layers == 0
+                or elements_per_layer == 0 or not self._fixed_mode()):
+            return False
+        for size, idx in zip(group_sizes, layer_indices):
+            if int(size) == 0 or not self._layer_index_ok(idx, source_layers):
+                return False
+        if sum(int(s) for s in group_sizes) != batch:
+            return False
+        source_elements = prefix_count * source_layers * elements_per_layer
+        for comp, size, out in zip(compressed_buffers, compressed_sizes,
+                                   output_tensors):
+            if (not self._on_device(comp) or int(size) == 0
+                    or not self._on_device(out)
+                    or out.dtype != torch.bfloat16 or not out.is_contiguous()
+                    or out.numel() < source_elements):
+                return False
+        rc = self._ctx.decompress_indexed_scatter_groups(
+            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
+            kvszp.u64_array([int(s) for s in compressed_sizes]),
+            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
+            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
+            kvszp.ptr_array([t.data_ptr() for t in layer_indices]),
+            kvszp.size_array([t.numel() for t in layer_indices]),
+            kvszp.size_array([int(s) for s in group_sizes]),
+            len(group_sizes), prefix_count, source_layers,
+            elements_per_layer, _stream_handle(self._device_id))
+        if rc != kvszp.OK:
+            _report("grouped indexed fixed BF16 scatter decompression failed")
+            return False
+        return True
+
     def synchronize(self) -> bool:
         """Waits for the current stream and reports device-side errors of
         earlier (enqueue-only) decompress calls.  No reference counterpart."""

@@ -59,6 +59,8 @@ EXPORTS = [
      [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _sz, _vp]),
     ("kvszp_decompress_batch_fixed_bf16_indexed_scatter", _i,
      [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
+    ("kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups", _i,
+     [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
     ("kvszp_synchronize", _i, [_vp, _vp]),
     ("kvszp_enable_timing", _i, [_vp, _i]),
     ("kvszp_drain_timing", _i, [_vp, _vp, _vp, _vp, _vp]),
@@ -226,6 +228,17 @@ class Context:
             self.handle, compressed, sizes, bounds, batch, destinations,
             layer_indices, selected_layers, prefix_count, source_layers,
             elements_per_layer, stream)
+
+    def decompress_indexed_scatter_groups(self, compressed, sizes, bounds,
+                                          batch, destinations, layer_indices,
+                                          selected_layers, group_sizes,
+                                          num_groups, prefix_count,
+                                          source_layers, elements_per_layer,
+                                          stream) -> int:
+        return self._lib.kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups(
+            self.handle, compressed, sizes, bounds, batch, destinations,
+            layer_indices, selected_layers, group_sizes, num_groups,
+            prefix_count, source_layers, elements_per_layer, stream)
 
     def synchronize(self, stream) -> int:
         return self._lib.kvszp_synchronize(self.handle, stream)

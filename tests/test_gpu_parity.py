@@ -159,8 +159,8 @@ def _encode(cpp, w, pages, eps):
     return bufs, sizes, bounds
 
 
-# 327683 and 1048576 elements: tiles past the decoder's direct-prefix range
-# take the look-back
+# 327683 and 1048576 elements: jobs of 40 and 128 tiles, so the persistent
+# decoder's runs of consecutive tiles start and end inside a job
 @pytest.mark.parametrize("n", [32, 77, 8192, 36864, 229376, 327683, 1048576])
 @pytest.mark.parametrize("rate0", [0, 1])
 def test_decompress_contiguous_matches_oracle(cpp, oracle, n, rate0):
@@ -253,6 +253,79 @@ def test_indexed_compress_and_scatter(cpp, oracle, prefix, src, epl, idx):
         stream = bufs[i][:sizes[i]].cpu().numpy()
         oracle.decompress_indexed(stream, n, bounds[i], want, idx, src, epl)
         assert np.array_equal(got[i], want), f"page {i}"
+
+
+@pytest.mark.parametrize("prefix,src,epl,groups", [
+    (2, 28, 4096, [[0, 1, 2, 5, 19, 20, 21],
+                   [3, 4, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 22,
+                    23, 24, 25, 26, 27]]),   # the mixed-bound restore
+    (2, 6, 100, [[5, 0], [3], [1, 2, 4]]),   # blocks straddle layers
+    (3, 4, 8200, [[2], [0, 3]]),             # partial tiles per job
+])
+def test_grouped_indexed_scatter_matches_oracle(cpp, oracle, prefix, src, epl,
+                                                groups):
+    """One grouped launch writes exactly what the per-group indexed scatter
+    calls write: every group's layers decoded, all other values untouched."""
+    per_group = [3, 2, 4][:len(groups)]
+    full = rand_pages(max(per_group), prefix * src * epl, seed=epl + 7)
+    w = make(cpp)
+    bufs, sizes, bounds, idx_t, dests, jobs = [], [], [], [], [], []
+    for g, layers in enumerate(groups):
+        it = torch.tensor(layers, dtype=torch.long, device=DEV)
+        n = prefix * len(layers) * epl
+        b = buffers(cpp, per_group[g], n)
+        eps = [1e-4, 1e-5, 1e-3, 2e-4][:per_group[g]]
+        ok, s, e = w.compress_batch_fixed_bf16_indexed(
+            list(full[:per_group[g]]), b, it, prefix, src, epl, eps)
+        assert ok
+        bufs += b
+        sizes += list(s)
+        bounds += list(e)
+        idx_t.append(it)
+        jobs += [(layers, n, i) for i in range(per_group[g])]
+    dest = torch.full((len(jobs), prefix * src * epl), -2.0,
+                      dtype=torch.bfloat16, device=DEV)
+    assert w.decompress_batch_fixed_bf16_indexed_scatter_groups(
+        bufs, sizes, list(dest), idx_t, per_group, prefix, src, epl, bounds)
+    assert w.synchronize()
+    got = u16(dest)
+    for k, (layers, n, _) in enumerate(jobs):
+        want = u16(torch.full((prefix * src * epl,), -2.0, dtype=torch.bfloat16))
+        stream = bufs[k][:sizes[k]].cpu().numpy()
+        oracle.decompress_indexed(stream, n, bounds[k], want, layers, src, epl)
+        assert np.array_equal(got[k], want), f"job {k}"
+    # the same jobs through the per-group calls give the same values
+    ref = torch.full_like(dest, -2.0)
+    k = 0
+    for it, cnt in zip(idx_t, per_group):
+        assert w.decompress_batch_fixed_bf16_indexed_scatter(
+            bufs[k:k + cnt], sizes[k:k + cnt], list(ref[k:k + cnt]), it,
+            prefix, src, epl, bounds[k:k + cnt])
+        k += cnt
+    assert w.synchronize()
+    assert np.array_equal(u16(ref), got)
+
+
+def test_grouped_indexed_scatter_rejects_bad_groups(cpp):
+    full = rand_pages(2, 2 * 4 * 64, seed=3)
+    w = make(cpp)
+    it = torch.tensor([1, 2], dtype=torch.long, device=DEV)
+    n = 2 * 2 * 64
+    bufs = buffers(cpp, 2, n)
+    ok, sizes, bounds = w.compress_batch_fixed_bf16_indexed(
+        list(full), bufs, it, 2, 4, 64, [1e-4, 1e-4])
+    assert ok
+    dest = list(torch.zeros_like(full))
+    # group sizes that do not cover the batch, an empty group, a group of
+    # more layers than the source holds
+    assert not w.decompress_batch_fixed_bf16_indexed_scatter_groups(
+        bufs, sizes, dest, [it], [1], 2, 4, 64, bounds)
+    assert not w.decompress_batch_fixed_bf16_indexed_scatter_groups(
+        bufs, sizes, dest, [it, it], [2, 0], 2, 4, 64, bounds)
+    big = torch.arange(5, dtype=torch.long, device=DEV) % 4
+    assert not w.decompress_batch_fixed_bf16_indexed_scatter_groups(
+        bufs, sizes, dest, [big], [2], 2, 4, 64, bounds)
+    assert w.synchronize()
 
 
 def test_indexed_groups_match_oracle(cpp, oracle):
