@@ -460,14 +460,17 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     p.bound_mode = bound_mode;
     p.quantizer = c->quantizer;
     p.aligned16 = aligned16 ? 1 : 0;
-    if (bound_mode != kBoundPrepass && c->pipelined_grid != 0 && whole_blocks &&
-        aligned16 && max_tiles_per_job <= c->pipelined_grid / 2) {
+    const bool persistent = bound_mode != kBoundPrepass && c->pipelined_grid != 0 &&
+                            whole_blocks && aligned16 &&
+                            max_tiles_per_job <= c->pipelined_grid / 2;
+    if (persistent) {
         // Persistent encoder (whole, aligned, single-layer blocks only); its
         // waits are cycle-free while a job's tiles number at most the grid
         // (half of it here, for margin).
-        p.ticket = nullptr;
+        CompressParams pp = p;
+        pp.ticket = nullptr;
         const uint32_t grid = (uint32_t)std::min<uint64_t>(total_tiles, c->pipelined_grid);
-        e = launch_compress_pipelined(p, grid, stream, timing_start(c, rec),
+        e = launch_compress_pipelined(pp, grid, stream, timing_start(c, rec),
                                       timing_stop(c, rec));
     } else {
         e = launch_compress(p, stream,
@@ -481,6 +484,19 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     // since callers need the sizes on the host (cuszp_wrapper.cpp:520-532).
     e = wait_stream(stream);
     if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
+    if (persistent && __atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq) {
+        // Some wave's payload was too large for the persistent encoder's
+        // staging words (rates near 31 throughout): encode the launch again
+        // with one workgroup per tile, under a fresh epoch.
+        if ((rc = next_epoch(c, stream, &epoch))) return rc;
+        p.epoch = epoch;
+        p.ticket_base = c->ticket_next;
+        e = launch_compress(p, stream, nullptr, timing_stop(c, rec));
+        if (e != hipSuccess) return hip_fail(e, "compress launch");
+        c->ticket_next += total_tiles;
+        e = wait_stream(stream);
+        if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
+    }
     rc = consume_device_error(c, stream);
     if (rc) return rc;
     for (size_t i = 0; i < batch; ++i) {

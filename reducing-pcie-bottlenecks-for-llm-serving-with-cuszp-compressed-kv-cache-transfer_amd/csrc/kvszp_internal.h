@@ -68,6 +68,7 @@ struct Group {
 // which tells the host that the table copy queued before it has completed.
 constexpr int kHostErrorMarker = 0;
 constexpr int kHostSeq = 1;
+constexpr int kHostOverflow = 2;  // seq of a persistent encode that must be redone
 constexpr int kHostCtlWords = 16;
 
 struct CompressJob {

@@ -183,14 +183,6 @@ __device__ __forceinline__ uint32_t cvt_abs_u32(float t) {
     return c;
 }
 
-// Field 2|q| + sign of quantize<kQuant>(x, recip), for |t| < 2^31
-// (field_sign / field_from_trunc state the identity).
-template <int kQuant>
-__device__ __forceinline__ uint32_t quant_field(float x, float recip) {
-    const float t = kQuant ? __builtin_fmaf(x, recip, 0.5f) : x * recip + 0.5f;
-    return field_from_trunc(cvt_abs_u32(t), field_sign(t, kQuant));
-}
-
 __device__ __forceinline__ float bf16_lo(uint32_t d) {
     return __uint_as_float(d << 16);
 }
@@ -462,19 +454,9 @@ __device__ __forceinline__ void lookback_publish(unsigned long long* state,
 // back over earlier tiles of the job 64 at a time until it meets one whose
 // inclusive prefix is published, publishes this tile's inclusive prefix and
 // returns the exclusive one (bytes of earlier tiles of the job).
-// lookback_first: the first window's words (what lookback_wait reads first),
-// for a caller that issues that read early to overlap it with other waits.
-__device__ __forceinline__ unsigned long long lookback_first(
-    const unsigned long long* state, uint32_t t, uint32_t tile) {
-    const uint32_t lane = __lane_id();
-    return (tile != 0 && lane < (tile < 64u ? tile : 64u)) ? load_relaxed(&state[t - 1 - lane])
-                                                          : 0ull;
-}
-
 __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
                                   uint32_t tile, uint32_t total, uint32_t epoch,
-                                  uint32_t* err, uint32_t* host_ctl,
-                                  bool have_first = false, unsigned long long first = 0) {
+                                  uint32_t* err, uint32_t* host_ctl) {
     if (tile == 0) return 0;
     const int lane = __lane_id();
     const uint32_t tag_agg = epoch * 4u + 1u;
@@ -489,12 +471,7 @@ __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
             nwin == 64u ? ~0ull : ((1ull << nwin) - 1ull);
         unsigned long long w = 0, need = 0, incl = 0;
         for (uint32_t spins = 0;; ++spins) {
-            if (have_first) {  // the caller's early read of this window
-                w = first;
-                have_first = false;
-            } else {
-                w = in_win ? load_relaxed(&state[pos - lane]) : 0ull;
-            }
+            w = in_win ? load_relaxed(&state[pos - lane]) : 0ull;
             const uint32_t tag = (uint32_t)(w >> 32);
             incl = __ballot(in_win && tag == tag_inc);
             const unsigned long long ready =
@@ -655,28 +632,6 @@ __device__ __forceinline__ void build_rows_lo_chained(const uint32_t* d, float r
         const uint32_t m0 = magnitude(q0), m1 = magnitude(q1);
         orv |= m0 | m1;
         P[k] = field_lo(m0, (uint32_t)q0 >> 31) | (field_lo(m1, (uint32_t)q1 >> 31) << 16);
-        prev = P[k];
-    }
-}
-
-// Rows of low fields for a full block whose |t| all stay below 2^31, and
-// the OR of the whole fields (its value >> 1 is the OR of all |q|).  Rows
-// are chained through the block's data words rather than the reciprocal
-// (no register copy per row).
-template <int kQuant>
-__device__ __forceinline__ void build_rows_fast_chained(uint32_t* d, float recip,
-                                                        uint32_t* P, uint32_t& orf) {
-    uint32_t prev = 0;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const int e0 = row_lo_elem(k), e1 = row_hi_elem(k);
-        asm volatile("" : "+v"(d[e0 >> 1]), "+v"(d[e1 >> 1]) : "v"(prev));
-        const float x0 = (e0 & 1) ? bf16_hi(d[e0 >> 1]) : bf16_lo(d[e0 >> 1]);
-        const float x1 = (e1 & 1) ? bf16_hi(d[e1 >> 1]) : bf16_lo(d[e1 >> 1]);
-        const uint32_t f0 = quant_field<kQuant>(x0, recip);
-        const uint32_t f1 = quant_field<kQuant>(x1, recip);
-        orf |= f0 | f1;
-        P[k] = __builtin_amdgcn_perm(f1, f0, 0x05040100u);  // low halves
         prev = P[k];
     }
 }
@@ -1115,100 +1070,10 @@ __device__ __forceinline__ uint32_t block_keys(const uint32_t* d, bool exists,
     return (kmin << 16) | kmax;
 }
 
-// Tile min/max: this thread's keys -> the tile's epoch-tagged word (one
-// barrier).
-__device__ __forceinline__ void publish_tile_keys(const CompressParams& p,
-                                                  uint32_t t, uint32_t kmin,
-                                                  uint32_t kmax, uint32_t* s_min,
-                                                  uint32_t* s_max, int tid) {
-    const int lane = tid & 63, wave = tid >> 6;
-    kmin = wave_min(kmin);
-    kmax = wave_max(kmax);
-    if (lane == 0) {
-        s_min[wave] = kmin;
-        s_max[wave] = kmax;
-    }
-    __syncthreads();
-    if (tid == 0) {
-#pragma unroll
-        for (int w = 1; w < kThreads / 64; ++w) {
-            kmin = s_min[w] < kmin ? s_min[w] : kmin;
-            kmax = s_max[w] > kmax ? s_max[w] : kmax;
-        }
-        store_relaxed(&p.tile_minmax[t],
-                      ((unsigned long long)p.epoch << 32) | (kmin << 16) | kmax);
-    }
-}
-
-// Min/max keys over all tiles of the job (one barrier); thread i < tiles
-// polls tile i's word.
-__device__ __forceinline__ void exchange_minmax(const CompressParams& p,
-                                                uint32_t first_t, uint32_t tiles,
-                                                uint32_t* s_min, uint32_t* s_max,
-                                                uint32_t& kmin, uint32_t& kmax,
-                                                int tid) {
-    const int lane = tid & 63, wave = tid >> 6;
-    kmin = kKeyEmptyMin;
-    kmax = kKeyEmptyMax;
-    if ((uint32_t)tid < tiles) {
-        const unsigned long long* slot = &p.tile_minmax[first_t + tid];
-        unsigned long long w = load_relaxed(slot);
-        for (uint32_t spins = 0; (uint32_t)(w >> 32) != p.epoch; ++spins) {
-            if (spins >= kSpinLimit) {
-                flag_error(p.error, p.host_ctl, kErrSpin);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-            w = load_relaxed(slot);
-        }
-        kmin = (uint32_t)(w >> 16) & 0xFFFFu;
-        kmax = (uint32_t)w & 0xFFFFu;
-    }
-    kmin = wave_min(kmin);
-    kmax = wave_max(kmax);
-    if (lane == 0) {
-        s_min[wave] = kmin;
-        s_max[wave] = kmax;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) {
-        kmin = s_min[w] < kmin ? s_min[w] : kmin;
-        kmax = s_max[w] > kmax ? s_max[w] : kmax;
-    }
-}
-
-// Keys of -inf (min) and +inf (max): every |x * recip| is infinite, so the
-// block counts as outside the monotone range.
+// Keys of -inf (min) and +inf (max), kept as the keys of a block holding a
+// NaN: they mark the block so that its wave takes the exact quantizer.
 constexpr uint32_t kNanRateKeys = (0x007Fu << 16) | 0xFF80u;
 
-// Rate of a block from its keys (see b. above; the caller checked that no
-// |x * recip| of the block reaches 2^30 and that it holds no NaN).
-template <int kQuant>
-__device__ __forceinline__ uint32_t rate_from_keys(uint32_t keys, float recip) {
-    const uint32_t m = max(magnitude(quantize<kQuant>(key_value(keys >> 16), recip)),
-                           magnitude(quantize<kQuant>(key_value(keys & 0xFFFFu), recip)));
-    return m ? 32u - (uint32_t)__builtin_clz(m) : 0u;
-}
-
-// Rate of a block by quantizing every value (NaN, saturation, wrap).
-template <int kQuant>
-__device__ __forceinline__ uint32_t rate_by_quantizing(const uint32_t* d, float recip) {
-    uint32_t orv = 0;
-#pragma unroll
-    for (int v = 0; v < kBlockElems; ++v)
-        orv |= magnitude(quant_elem<kQuant, true>(d, v, kBlockElems, recip));
-    return orv ? 32u - (uint32_t)__builtin_clz(orv) : 0u;
-}
-
-// Rows of 16-bit fields (sign << 15) | |q| for a block whose |q| < 2^15 and
-// whose |t| < 2^31 (quant_field's identity): row k holds elements k^7 (low
-// half) and 16+(k^7) (high half).  After transpose16x2, rows 0..14 are planes
-// 0..14 (stream words w_1..w_15) and row 15 is the sign word w_0.  The two-
-// roundings sign test t < 0 is t's sign bit (t is never -0.0: v + 0.5 = 0
-// rounds to +0.0; the caller excludes NaN).  Rows are chained through the
-// block's words (an empty asm) so the scheduler does not start all 32
-// conversions at once.
 // a * b + c for a, b < 2^24 as one instruction (the compiler otherwise
 // expands s * 0x8001 for a 0/1 value s into an arithmetic shift and an AND).
 __device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
@@ -1217,6 +1082,14 @@ __device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) 
     return d;
 }
 
+// Rows of 16-bit fields (sign << 15) | |q| for a block whose |q| < 2^15 and
+// whose |t| < 2^31 (the identity stated at field_sign in kvszp_bits.h): row
+// k holds elements k^7 (low half) and 16+(k^7) (high half).  After
+// transpose16x2, rows 0..14 are planes 0..14 (stream words w_1..w_15) and
+// row 15 is the sign word w_0.  The two-roundings sign test t < 0 is t's
+// sign bit (t is never -0.0: v + 0.5 = 0 rounds to +0.0; the caller excludes
+// NaN).  Rows are chained through the block's words (an empty asm) so the
+// scheduler does not start all 32 conversions at once.
 template <int kQuant>
 __device__ __forceinline__ void build_rows_signhi(uint32_t* d, float recip, uint32_t* P) {
     constexpr uint32_t kSignHi = 0x8001u;
@@ -1242,13 +1115,93 @@ __device__ __forceinline__ void build_rows_signhi(uint32_t* d, float recip, uint
     }
 }
 
-// A wave's payload staged in LDS: lane l's block is words [off, off + count)
-// of the wave's payload.  The stream words are the transposed rows P:
+// Tile-level facts of the tile whose payload waits in the staging words.
+struct PendingTile {
+    uint32_t t, tile, job, total, R, last, first;
+    float eb;
+    uint8_t* out;
+};
+
+// ---- persistent encoder --------------------------------------------------------
+// Two waves per workgroup and two blocks per thread: lane l of wave w holds
+// blocks 128w + l and 128w + 64 + l of the tile (its 64-block runs 2w and
+// 2w + 1).  The per-tile work that does not grow with the block count (bound
+// exchange, scan, look-back, tile bookkeeping) is then shared by 128 blocks
+// per wave.
+constexpr int kEncThreads = 128;
+constexpr int kEncWaves = kEncThreads / 64;
+constexpr int kEncStageWords = 2 * 64 * 16 + 16;  // 128 blocks of <= 16 words
+
+// Largest fl(|x| * recip) for which every value of a job quantizes to a
+// sign-high field: |t| <= 32766.5 gives |q| = c + s <= 32767 < 2^15 (for
+// either quantizer; fl and fma round monotonically).
+constexpr float kFastLimit = 32766.0f;
+
+// Wave 0: the min/max keys over all tiles of the job (lane i polls tiles
+// i, i + 64, ...; all lanes end together).
+__device__ __forceinline__ void job_keys(const CompressParams& p, uint32_t first_t,
+                                         uint32_t tiles, int lane, uint32_t& kmin,
+                                         uint32_t& kmax) {
+    kmin = kKeyEmptyMin;
+    kmax = kKeyEmptyMax;
+    for (uint32_t i = (uint32_t)lane; i < tiles; i += 64u) {
+        const unsigned long long* slot = &p.tile_minmax[first_t + i];
+        unsigned long long w = load_relaxed(slot);
+        for (uint32_t spins = 0; (uint32_t)(w >> 32) != p.epoch; ++spins) {
+            if (spins >= kSpinLimit) {
+                flag_error(p.error, p.host_ctl, kErrSpin);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            w = load_relaxed(slot);
+        }
+        const uint32_t lo = (uint32_t)(w >> 16) & 0xFFFFu, hi = (uint32_t)w & 0xFFFFu;
+        kmin = lo < kmin ? lo : kmin;
+        kmax = hi > kmax ? hi : kmax;
+    }
+    kmin = wave_min(kmin);
+    kmax = wave_max(kmax);
+}
+
+// A tile's min/max keys out (one barrier): both waves reduce their lanes'
+// keys, thread 0 combines and publishes the epoch-tagged word.
+__device__ __forceinline__ void publish_keys2(const CompressParams& p, uint32_t t,
+                                              uint32_t kmin, uint32_t kmax,
+                                              uint32_t* s_min, uint32_t* s_max,
+                                              int wave, int lane) {
+    kmin = wave_min(kmin);
+    kmax = wave_max(kmax);
+    if (lane == 0) {
+        s_min[wave] = kmin;
+        s_max[wave] = kmax;
+    }
+    __syncthreads();
+    if (wave == 0 && lane == 0) {
+        kmin = s_min[1] < kmin ? s_min[1] : kmin;
+        kmax = s_max[1] > kmax ? s_max[1] : kmax;
+        store_relaxed(&p.tile_minmax[t],
+                      ((unsigned long long)p.epoch << 32) | (kmin << 16) | kmax);
+    }
+}
+
+// Rate of a block from its sign-high field rows (before the transpose): the
+// OR of the rows has the bit length of the largest |q| in its low 15 bits
+// of either half.
+__device__ __forceinline__ uint32_t rate_of_rows(const uint32_t* P) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) o |= P[k];
+    const uint32_t m = (o | (o >> 16)) & 0x7FFFu;
+    return m ? 32u - (uint32_t)__builtin_clz(m) : 0u;
+}
+
+// A wave's payload staged in LDS: the block is words [off, off + count) of
+// the wave's payload.  The stream words are the transposed rows P:
 // w_j = P[j] (kSignHi false), or w_0 = P[15] and w_j = P[j - 1] (sign-high
 // rows).  Words are written from the highest index down: a lane's unused
-// slots (index >= count) only ever fall on later lanes' words, which are
+// slots (index >= count) only ever fall on words of later blocks, which are
 // written afterwards, or past the payload end, so `stage` needs room for
-// 1024 + 16 words.
+// the payload plus 16 words.
 template <bool kSignHi>
 __device__ __forceinline__ void stage_payload(const uint32_t* P, uint32_t count,
                                               uint32_t off, uint32_t cmax,
@@ -1264,58 +1217,88 @@ __device__ __forceinline__ void stage_payload(const uint32_t* P, uint32_t count,
 }
 
 // Writes a wave's staged payload (`words` words) to `dst` (4-byte aligned):
-// word w goes out from lane w mod 64, so every store covers 256 contiguous
-// bytes and every LDS read 64 consecutive words (no bank conflicts).
+// lane l moves words 4l .. 4l + 3 of every 256-word chunk with one 16-byte
+// LDS read and one 16-byte store (each store instruction covers 1 KiB of
+// contiguous stream), then lanes 0..2 the last words.
 __device__ __forceinline__ void copy_payload(uint32_t* dst, uint32_t words,
                                              const uint32_t* stage, int lane) {
     __builtin_amdgcn_wave_barrier();
     __asm__ volatile("" ::: "memory");
     g_u32* d = to_global(dst);
-    for (uint32_t w = (uint32_t)lane; w < words; w += 64u) d[w] = stage[w];
+    const uint32_t quads = words >> 2;
+    for (uint32_t q = (uint32_t)lane; q < quads; q += 64u)
+        *(g_u32x4_a4*)(d + 4u * q) = *(const u32x4*)(stage + 4u * q);
+    const uint32_t tail = 4u * quads + (uint32_t)lane;
+    if (tail < words) d[tail] = stage[tail];
     __builtin_amdgcn_wave_barrier();
     __asm__ volatile("" ::: "memory");  // before the words are reused
 }
 
-// Tile-level facts of the tile whose payload waits in the staging words.
-struct PendingTile {
-    uint32_t t, tile, job, total, R, last, first;
-    float eb;
-    uint8_t* out;
-};
+// Words 16 .. count - 1 of a block (rates above 15), exactly (no slot past
+// `count` is written: the low words of later blocks are already in place).
+__device__ __forceinline__ void stage_high_words(const uint32_t* P, uint32_t count,
+                                                 uint32_t off, uint32_t* stage) {
+    __asm__ volatile("" ::: "memory");
+    uint32_t* s = stage + off + 16;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        if ((uint32_t)j + 16u < count) s[j] = P[j];
+    __asm__ volatile("" ::: "memory");
+}
 
-// Five waves per SIMD (at most 96 VGPRs, no scratch).
+// Rows of one block (cu:180-231) and its rate.  Fast path: sign-high rows
+// (sign << 15) | |q|, whose transpose gives planes 0..14 then the sign word.
+// Otherwise the exact quantizer's low fields ((|q| << 1) | sign) & 0xFFFF,
+// whose transpose gives words 0..15 in stream order.  Either way the rate is
+// the bit length of the OR of |q|.
+template <int kQuant>
+__device__ __forceinline__ uint32_t block_rows(uint32_t* d, float recip, bool fast,
+                                               uint32_t* P) {
+    if (fast) {
+        build_rows_signhi<kQuant>(d, recip, P);
+        return rate_of_rows(P);
+    }
+    uint32_t o = 0;
+    build_rows_lo_chained<kQuant>(d, recip, P, o);
+    return o ? 32u - (uint32_t)__builtin_clz(o) : 0u;
+}
+
+// Three waves per SIMD (at most 168 VGPRs, no scratch).
+//
+// Per tile: (a) wave 0 gathers the job's min/max and works out the bound
+// while wave 1 finishes the look-back of the tile staged one iteration
+// earlier; (d) that tile's payload out; (b) per 64-block half of each wave:
+// rows, rates, the wave scan, staging; then the tile scan, header and
+// aggregate out; (c) the next tile's keys out and the tile after it loading.
 //
 // Deferred stores: a tile's payload is staged in LDS at wave-relative
 // offsets and written out one iteration later, after the tile's look-back,
 // which by then normally finds its predecessors' prefixes published and does
-// not wait.  The look-back of tile t - G runs in wave 0 before tile t's scan,
-// whose barrier hands the prefix to the other waves.  A tile with a rate
-// above 15 (payload too large to stage) is stored at once instead, after its
-// own look-back.
+// not wait.  Staging needs only the wave's own offsets, so each half is
+// staged as soon as its rows exist and no more than one half's rows are held.
 //
 // Wait order with deferral (ranks increase along every workgroup's program):
 // the exchange of tile t has rank t, the look-back of t rank t + G + 1/2.
 // The look-back of t needs the aggregates of tiles x < t, published after the
-// exchange of x (rank x) and look-backs of rank <= x - G + 1/2; the exchange of
-// t needs the min/max of tiles u of t's job, published after the exchange of
-// u - G (rank u - G < t, as u < t + G/2) and look-backs of rank <= u - 2G +
-// 1/2.  Every wait depends only on waits of lower rank: no cycle while all
-// G workgroups are resident.
+// exchange of x (rank x) and look-backs of rank <= x - G + 1/2; the exchange
+// of t needs the min/max of tiles u of t's job, published after the exchange
+// of u - G (rank u - G < t, as u < t + G/2) and look-backs of rank <=
+// u - 2G + 1/2.  Every wait depends only on waits of lower rank: no cycle
+// while all G workgroups are resident.
 template <int kQuant>
-__global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
+__global__ __launch_bounds__(kEncThreads)
+__attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
     CompressParams p) {
-    constexpr int kStageWords = 1024 + 16;
-    __shared__ uint32_t s_wave[2][kThreads / 64];
-    __shared__ uint32_t s_wmax[2][kThreads / 64];
-    __shared__ uint32_t s_min[kThreads / 64], s_max[kThreads / 64];    // publish
-    __shared__ uint32_t s_xmin[kThreads / 64], s_xmax[kThreads / 64];  // exchange
-    __shared__ uint32_t s_prefix[3];  // by tile parity; [2] for the last tile
+    __shared__ uint32_t s_wave[2][kEncWaves];
+    __shared__ uint32_t s_min[kEncWaves], s_max[kEncWaves];
+    __shared__ float s_bnd[2][2];      // by tile parity: eb, recip
+    __shared__ uint32_t s_fast[2];     // by tile parity: job on the fast path
+    __shared__ uint32_t s_prefix[3];   // by tile parity; [2] for the last tile
     __shared__ uint32_t s_gfirst[kMaxGroups];
     __shared__ uint8_t s_rate[2][kTileBlocks];
     __shared__ PendingTile s_pend[2];  // by the parity of the tile it holds
-    __shared__ uint32_t s_pwave[kThreads / 64][2];  // staged: wave offset, words
-    __shared__ __attribute__((aligned(16))) uint32_t s_stage[kThreads / 64][kStageWords];
+    __shared__ uint32_t s_pwave[kEncWaves][2];  // staged: wave offset, words
+    __shared__ __attribute__((aligned(16))) uint32_t s_stage[kEncWaves][kEncStageWords];
 
     publish_seq(p.host_ctl, p.seq);
     if ((int)threadIdx.x < p.num_groups) s_gfirst[threadIdx.x] = p.groups[threadIdx.x].first_tile;
@@ -1326,68 +1309,83 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
 
     // Prologue: the first tile and its keys (published), the next one loading.
     TileCtx cur = tile_ctx(p, blockIdx.x, s_gfirst);
-    uint32_t D[16], N[16];
-    // Rate keys of the current tile's blocks: the published keys, except
-    // that a block holding a NaN keeps the keys of -inf and +inf, which
-    // sends its wave down the exact path in b.
-    uint32_t keys;
+    uint32_t D0[16], D1[16], N0[16], N1[16];
+    // Keys of the current tile's blocks: the published keys, except that a
+    // block holding a NaN keeps the keys of -inf and +inf (kNanRateKeys),
+    // which keeps its wave off the fast path.
+    uint32_t keys0, keys1;
     bool has_next;
     TileCtx nxt;
     {
         const int tid = loop_tid();
+        const int lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const Group& g = p.groups[cur.gi];
-        load_block_regs(p, cur, g, wave, tid & 63, D);
-        uint32_t nan;
-        keys = block_keys(D, block_exists(g, cur.tile, tid), nan);
-        if (fused) publish_tile_keys(p, cur.t, keys >> 16, keys & 0xFFFFu, s_min, s_max, tid);
-        if (nan) keys = kNanRateKeys;
+        load_block_regs(p, cur, g, 2 * wave, lane, D0);
+        load_block_regs(p, cur, g, 2 * wave + 1, lane, D1);
+        uint32_t nan0, nan1;
+        keys0 = block_keys(D0, block_exists(g, cur.tile, 128 * wave + lane), nan0);
+        keys1 = block_keys(D1, block_exists(g, cur.tile, 128 * wave + 64 + lane), nan1);
+        if (fused)
+            publish_keys2(p, cur.t, min(keys0 >> 16, keys1 >> 16),
+                          max(keys0 & 0xFFFFu, keys1 & 0xFFFFu), s_min, s_max, wave, lane);
+        if (nan0) keys0 = kNanRateKeys;
+        if (nan1) keys1 = kNanRateKeys;
         has_next = cur.t + G < p.total_tiles;
         if (has_next) {
             nxt = tile_ctx(p, cur.t + G, s_gfirst);
-            load_block_regs(p, nxt, p.groups[nxt.gi], wave, tid & 63, N);
+            const Group& gn = p.groups[nxt.gi];
+            load_block_regs(p, nxt, gn, 2 * wave, lane, N0);
+            load_block_regs(p, nxt, gn, 2 * wave + 1, lane, N1);
         }
     }
 
+    // One tile.  X holds this tile's values, Y the next tile's (loading since
+    // the previous iteration); the tile after that is loaded into X once X
+    // is no longer needed, and the next call swaps the roles (no copies).
     uint32_t parity = 0;
-    for (;; parity ^= 1u) {
+    auto iteration = [&](uint32_t (&X0)[16], uint32_t (&X1)[16], uint32_t (&Y0)[16],
+                         uint32_t (&Y1)[16]) -> bool {
         const int tid = loop_tid();
         const int lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const Group& g = p.groups[cur.gi];
-        const bool ex = block_exists(g, cur.tile, tid);
+        const uint32_t blk0 = 128u * (uint32_t)wave + (uint32_t)lane;
 
         // The tile loaded at c. (two ahead): its context and this wave's
-        // source now, so that the scalar loads and divisions overlap the
-        // exchange below.
+        // sources now, so that the scalar loads and divisions overlap the
+        // waits below.
         const bool has_after = has_next && nxt.t + G < p.total_tiles;
         TileCtx after = nxt;
-        WaveSource asrc{nullptr};
+        WaveSource asrc0{nullptr}, asrc1{nullptr};
         if (has_after) {
             after = tile_ctx(p, nxt.t + G, s_gfirst);
-            asrc = wave_source(p, after, p.groups[after.gi], wave);
+            const Group& ga = p.groups[after.gi];
+            asrc0 = wave_source(p, after, ga, 2 * wave);
+            asrc1 = wave_source(p, after, ga, 2 * wave + 1);
         }
 
-        // a. bound; wave 0 also finishes the pending tile's look-back (its
-        // first read issued before the exchange's, so the two overlap)
-        unsigned long long lb_first = 0;
-        if (pending && wave == 0) {
-            const PendingTile& q = s_pend[parity ^ 1u];
-            lb_first = lookback_first(p.tile_state, q.t, q.tile);
-        }
-        float eb = job_of(p, cur).eps;
-        if (fused) {
-            uint32_t kmin, kmax;
-            exchange_minmax(p, cur.t - cur.tile, g.tiles_per_job, s_xmin, s_xmax,
-                            kmin, kmax, tid);
-            eb = relative_bound(job_of(p, cur).eps, kmin, kmax);
-        }
-        const float recip = 0.5f / eb;  // cu:166, IEEE division
-        if (pending && wave == 0) {
+        // a. wave 0: the bound; wave 1: the pending tile's look-back.
+        if (wave == 0) {
+            const float eps = job_of(p, cur).eps;
+            float eb = eps;
+            uint32_t fast = 0;
+            if (fused) {
+                uint32_t kmin, kmax;
+                job_keys(p, cur.t - cur.tile, g.tiles_per_job, lane, kmin, kmax);
+                eb = relative_bound(eps, kmin, kmax);
+                const float jabs = fmaxf(fabsf(min_key_value(kmin)), fabsf(max_key_value(kmax)));
+                fast = jabs * (0.5f / eb) <= kFastLimit ? 1u : 0u;
+            }
+            if (lane == 0) {
+                s_bnd[parity][0] = eb;
+                s_bnd[parity][1] = 0.5f / eb;  // cu:166, IEEE division
+                s_fast[parity] = fast;
+            }
+        } else if (pending) {
             const PendingTile& q = s_pend[parity ^ 1u];
             const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                              p.epoch, p.error, p.host_ctl, true,
-                                              lb_first);
+                                              p.epoch, p.error, p.host_ctl);
             if (lane == 0) {
                 s_prefix[parity] = pf;
                 if (q.last)
@@ -1398,24 +1396,86 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
                                        __HIP_MEMORY_SCOPE_SYSTEM);
             }
         }
+        __syncthreads();
 
-        // b. rates, tile scan, header bytes (padding zeroed by the last
-        // tile), aggregate out
-        const float bmax = fmaxf(fabsf(key_value(keys >> 16)), fabsf(key_value(keys & 0xFFFFu)));
-        const bool mono = !ex || fabsf(bmax * recip) < 0x1p30f;
-        const bool wave_mono = __ballot(!mono) == 0ull;  // wave-uniform
-        uint32_t rate = 0;
-        if (ex) rate = wave_mono ? rate_from_keys<kQuant>(keys, recip)
-                                 : rate_by_quantizing<kQuant>(D, recip);
-        const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
-        const uint32_t rmax = wave_max(rate);
-        s_rate[parity][tid] = (uint8_t)rate;
-        if (lane == 0) s_wmax[parity][wave] = rmax;
-        const TileScan sc = tile_scan(bytes, tid, s_wave[parity]);  // the barrier
-        uint32_t tile_rmax = 0;
+        // d. the pending tile's payload out (frees the staging words)
+        if (pending) {
+            const PendingTile& q = s_pend[parity ^ 1u];
+            const uint32_t woff = s_pwave[wave][0], words = s_pwave[wave][1];
+            if (words)
+                copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[parity] + woff),
+                             words, &s_stage[wave][0], lane);
+        }
+
+        // b. per half: rows, rate, the wave's offsets, staging (cu:302-358:
+        // sign word, then `rate` plane words).  Fast path when no block of
+        // the wave holds a NaN and every |x * recip| is at most kFastLimit,
+        // known for the whole job from its min/max or else from the keys.
+        const float eb = s_bnd[parity][0];
+        const float recip = s_bnd[parity][1];
+        bool fast_w = false;
+        if (__ballot(keys0 == kNanRateKeys || keys1 == kNanRateKeys) == 0ull) {
+            if (s_fast[parity] != 0) {
+                fast_w = true;
+            } else {
+                const bool ex0 = block_exists(g, cur.tile, (int)blk0);
+                const bool ex1 = block_exists(g, cur.tile, (int)blk0 + 64);
+                const float bmax0 = fmaxf(fabsf(key_value(keys0 >> 16)), fabsf(key_value(keys0 & 0xFFFFu)));
+                const float bmax1 = fmaxf(fabsf(key_value(keys1 >> 16)), fabsf(key_value(keys1 & 0xFFFFu)));
+                const bool ok = (!ex0 || bmax0 * recip <= kFastLimit) &&
+                                (!ex1 || bmax1 * recip <= kFastLimit);
+                fast_w = __ballot(!ok) == 0ull;
+            }
+        }
+        // A wave whose payload would not fit the staging words (rates far
+        // above 15 throughout) stages no more and tells the host, which
+        // encodes the whole launch again with the one-workgroup-per-tile
+        // kernel; the rest of this launch carries on normally.
+        uint32_t wave_bytes = 0;
+        bool overflow = false;
 #pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) tile_rmax = max(tile_rmax, s_wmax[parity][w]);
-        const bool wide_tile = tile_rmax > 15u;
+        for (int h = 0; h < 2; ++h) {
+            uint32_t (&X)[16] = h ? X1 : X0;
+            uint32_t P[16];
+            const uint32_t rate = block_rows<kQuant>(X, recip, fast_w, P);
+            const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
+            const uint32_t count = rate ? rate + 1u : 0u;
+            const uint32_t incl = wave_inclusive_scan(bytes, lane);
+            const uint32_t half_bytes = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+            const uint32_t rmax = wave_max(rate);
+            s_rate[parity][blk0 + 64u * h] = (uint8_t)rate;
+            const uint32_t off = (wave_bytes + incl - bytes) >> 2;  // words
+            wave_bytes += half_bytes;
+            overflow = overflow || (wave_bytes >> 2) + 16u > (uint32_t)kEncStageWords;
+            if (!overflow && rmax != 0) {
+                transpose16x2(P);
+                const uint32_t cmax = rmax < 15u ? rmax + 1u : 16u;
+                if (fast_w) {
+                    stage_payload<true>(P, count, off, cmax, &s_stage[wave][0]);
+                } else {
+                    stage_payload<false>(P, count < 16u ? count : 16u, off, cmax,
+                                         &s_stage[wave][0]);
+                    if (rmax > 15u) {
+                        // Words 16..31 (rates above 15, rare): high fields,
+                        // staged exactly.
+                        build_rows_hi_chained<kQuant>(X, recip, P);
+                        transpose16x2(P);
+                        stage_high_words(P, count, off, &s_stage[wave][0]);
+                    }
+                }
+            }
+        }
+        if (overflow && lane == 0)
+            __hip_atomic_store(&p.host_ctl[kHostOverflow], p.seq, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+
+        // Tile scan (the barrier), header bytes (padding zeroed by the last
+        // tile), aggregate out.
+        if (lane == 0) s_wave[parity][wave] = wave_bytes;
+        __syncthreads();
+        const uint32_t wb0 = s_wave[parity][0];
+        const uint32_t total = wb0 + s_wave[parity][1];
+        const uint32_t wave_off = wave ? wb0 : 0u;
         const uint32_t R = g.header_bytes;
         if (tid < kTileBlocks / 4) {
             const uint8_t* r = s_rate[parity];
@@ -1427,141 +1487,75 @@ __attribute__((amdgpu_waves_per_eu(5, 5))) void compress_persistent_kernel(
         const bool last_tile = cur.tile + 1 == g.tiles_per_job;
         if (last_tile) {
             for (uint32_t off = (cur.tile + 1) * kTileBlocks + 4u * tid; off < R;
-                 off += 4u * kThreads)
+                 off += 4u * kEncThreads)
                 *to_global(reinterpret_cast<uint32_t*>(job_of(p, cur).out + off)) = 0u;
         }
-        if (wave == 0) lookback_publish(p.tile_state, cur.t, cur.tile, sc.total, p.epoch);
-
-        // d. the pending tile's payload out (its prefix came with the scan)
-        if (pending) {
-            const PendingTile& q = s_pend[parity ^ 1u];
-            const uint32_t woff = s_pwave[wave][0], words = s_pwave[wave][1];
-            if (words)
-                copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[parity] + woff),
-                             words, &s_stage[wave][0], lane);
+        if (wave == 0) lookback_publish(p.tile_state, cur.t, cur.tile, total, p.epoch);
+        if (lane == 0) {
+            s_pwave[wave][0] = wave_off;
+            s_pwave[wave][1] = overflow ? 0u : wave_bytes >> 2;
         }
-
-        // Fields (cu:180-231).  signhi: (sign << 15) | |q| rows, whose
-        // transpose gives planes 0..14 then the sign word; otherwise
-        // ((|q| << 1) | sign) & 0xFFFF rows, whose transpose gives the words
-        // in stream order.
-        const bool signhi = wave_mono && rmax <= 15u;
-        uint32_t P[16];
-        if (rmax > 15u) {
-            // Rates 16..31 (rare): the high fields (|q| >> 15: planes 15..30,
-            // words w_16..w_31) are transposed and parked in the wave's
-            // staging words (free again after d.).
-            build_rows_hi_chained<kQuant>(D, recip, P);
-            transpose16x2(P);
-#pragma unroll
-            for (int j = 0; j < 16; ++j) s_stage[wave][64 * j + lane] = P[j];
+        // Written by the wave that reads it first (wave 1's look-back in the
+        // next iteration, or the flush below); wave 0 reads it only after the
+        // next barrier.
+        if (tid == 64) {
+            PendingTile q;
+            q.t = cur.t;
+            q.tile = cur.tile;
+            q.job = cur.job;
+            q.total = total;
+            q.R = R;
+            q.last = last_tile;
+            q.first = cur.tile == 0;
+            q.eb = eb;
+            q.out = job_of(p, cur).out;
+            s_pend[parity] = q;
         }
-        if (rmax != 0) {
-            if (signhi) {
-                build_rows_signhi<kQuant>(D, recip, P);
-            } else {
-                uint32_t orv = 0;
-                build_rows_lo_chained<kQuant>(D, recip, P, orv);
-            }
-        }
+        pending = true;
 
         // c. the next tile's keys and min/max (its loads were issued one
         // iteration ago and complete here); this tile's values are no longer
-        // needed, so the next tile moves into D and the one after it starts
-        // loading into N -- each load then has a whole iteration to arrive.
-        uint32_t nkeys = 0;
+        // needed, so the tile after the next one starts loading into X --
+        // each load then has a whole iteration to arrive.
+        uint32_t nkeys0 = 0, nkeys1 = 0;
         if (has_next) {
-            uint32_t nnan;
-            nkeys = block_keys(N, block_exists(p.groups[nxt.gi], nxt.tile, tid), nnan);
+            const Group& gn = p.groups[nxt.gi];
+            uint32_t nnan0, nnan1;
+            nkeys0 = block_keys(Y0, block_exists(gn, nxt.tile, (int)blk0), nnan0);
+            nkeys1 = block_keys(Y1, block_exists(gn, nxt.tile, (int)blk0 + 64), nnan1);
             if (fused)
-                publish_tile_keys(p, nxt.t, nkeys >> 16, nkeys & 0xFFFFu, s_min, s_max, tid);
-            if (nnan) nkeys = kNanRateKeys;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) D[i] = N[i];
-            if (has_after) load_block_from(p, after, p.groups[after.gi], asrc, wave, lane, N);
-        }
-
-        // e. payload (cu:302-358): sign word, then `rate` plane words.
-        // Waves with rates <= 15 stage theirs; it goes out next iteration,
-        // or, in a tile with a wider wave, right after this tile's look-back.
-        const uint32_t count = rate ? rate + 1u : 0u;
-        const uint32_t wave_off = __builtin_amdgcn_readfirstlane(sc.exclusive);
-        const uint32_t wave_words =
-            ((uint32_t)__builtin_amdgcn_readlane((int)(sc.exclusive + bytes), 63) - wave_off) >> 2;
-        if (rmax != 0 && rmax <= 15u) {
-            transpose16x2(P);
-            const uint32_t off = (sc.exclusive - wave_off) >> 2;
-            if (signhi)
-                stage_payload<true>(P, count, off, rmax + 1u, &s_stage[wave][0]);
-            else
-                stage_payload<false>(P, count, off, rmax + 1u, &s_stage[wave][0]);
-        }
-        if (!wide_tile) {
-            if (lane == 0) {
-                s_pwave[wave][0] = wave_off;
-                s_pwave[wave][1] = wave_words;
+                publish_keys2(p, nxt.t, min(nkeys0 >> 16, nkeys1 >> 16),
+                              max(nkeys0 & 0xFFFFu, nkeys1 & 0xFFFFu), s_min, s_max, wave, lane);
+            if (nnan0) nkeys0 = kNanRateKeys;
+            if (nnan1) nkeys1 = kNanRateKeys;
+            if (has_after) {
+                const Group& ga = p.groups[after.gi];
+                load_block_from(p, after, ga, asrc0, 2 * wave, lane, X0);
+                load_block_from(p, after, ga, asrc1, 2 * wave + 1, lane, X1);
             }
-            if (tid == 0) {
-                PendingTile q;
-                q.t = cur.t;
-                q.tile = cur.tile;
-                q.job = cur.job;
-                q.total = sc.total;
-                q.R = R;
-                q.last = last_tile;
-                q.first = cur.tile == 0;
-                q.eb = eb;
-                q.out = job_of(p, cur).out;
-                s_pend[parity] = q;
-            }
-            pending = true;
-        } else {
-            // This tile's look-back now (wave 0; one more barrier hands the
-            // prefix over).
-            if (wave == 0) {
-                const uint32_t pf = lookback_wait(p.tile_state, cur.t, cur.tile, sc.total,
-                                                  p.epoch, p.error, p.host_ctl);
-                if (lane == 0) {
-                    s_prefix[parity ^ 1u] = pf;
-                    if (last_tile)
-                        __hip_atomic_store(&p.host_sizes[cur.job], R + pf + sc.total,
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    if (cur.tile == 0)
-                        __hip_atomic_store(&p.host_bounds[cur.job], eb, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_SYSTEM);
-                }
-            }
-            __syncthreads();
-            uint8_t* base = job_of(p, cur).out + R + s_prefix[parity ^ 1u];
-            if (rmax > 15u) {
-                // Rates 16..31 (rare): each lane writes its own words, the low
-                // fields, then the parked high fields.
-                uint32_t* dst = reinterpret_cast<uint32_t*>(base + sc.exclusive);
-                transpose16x2(P);
-                store_words<16>(dst, P, count < 16u ? count : 16u, 16u);
-#pragma unroll
-                for (int j = 0; j < 16; ++j) P[j] = s_stage[wave][64 * j + lane];
-                store_words<16>(dst + 16, P, count > 16u ? count - 16u : 0u, rmax - 15u);
-            } else if (wave_words) {
-                copy_payload(reinterpret_cast<uint32_t*>(base + wave_off), wave_words,
-                             &s_stage[wave][0], lane);
-            }
-            pending = false;
         }
 
         // f. advance
-        if (!has_next) break;
+        if (!has_next) return false;
         cur = nxt;
-        keys = nkeys;
+        keys0 = nkeys0;
+        keys1 = nkeys1;
         has_next = cur.t + G < p.total_tiles;
-        if (has_next) nxt = tile_ctx(p, cur.t + G, s_gfirst);
+        if (has_next) nxt = after.t == cur.t + G ? after : tile_ctx(p, cur.t + G, s_gfirst);
+        return true;
+    };
+    for (;;) {
+        if (!iteration(D0, D1, N0, N1)) break;
+        parity ^= 1u;
+        if (!iteration(N0, N1, D0, D1)) break;
+        parity ^= 1u;
     }
     // The last staged payload.
     if (pending) {
         const int tid = loop_tid();
         const int lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-        if (wave == 0) {
+        if (wave == 1) {
             const PendingTile& q = s_pend[parity];
             const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
                                               p.epoch, p.error, p.host_ctl);
@@ -2149,13 +2143,20 @@ __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_
 // Launchers.  With timing events, hipExtLaunchKernelGGL stamps them with
 // the kernel's own start and end (no separate marker packets).
 template <class... Args>
-static void launch(void (*kernel)(Args...), uint32_t grid, hipStream_t stream,
-                   hipEvent_t start, hipEvent_t stop, Args... args) {
+static void launch_block(void (*kernel)(Args...), uint32_t grid, uint32_t block,
+                         hipStream_t stream, hipEvent_t start, hipEvent_t stop,
+                         Args... args) {
     if (start || stop)
-        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream,
+        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream,
                               start, stop, 0, args...);
     else
-        hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream, args...);
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream, args...);
+}
+
+template <class... Args>
+static void launch(void (*kernel)(Args...), uint32_t grid, hipStream_t stream,
+                   hipEvent_t start, hipEvent_t stop, Args... args) {
+    launch_block(kernel, grid, kThreads, stream, start, stop, args...);
 }
 
 hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
@@ -2171,9 +2172,9 @@ hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
                                      hipStream_t stream, hipEvent_t start,
                                      hipEvent_t stop) {
     if (p.quantizer)
-        launch(compress_persistent_kernel<1>, grid, stream, start, stop, p);
+        launch_block(compress_persistent_kernel<1>, grid, kEncThreads, stream, start, stop, p);
     else
-        launch(compress_persistent_kernel<0>, grid, stream, start, stop, p);
+        launch_block(compress_persistent_kernel<0>, grid, kEncThreads, stream, start, stop, p);
     return hipGetLastError();
 }
 
@@ -2232,8 +2233,8 @@ int compress_resident_workgroups(int device, bool pipelined) {
     const void* fn = pipelined
         ? reinterpret_cast<const void*>(compress_persistent_kernel<0>)
         : reinterpret_cast<const void*>(compress_kernel<0>);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0) !=
-        hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, fn, pipelined ? kEncThreads : kThreads, 0) != hipSuccess)
         per_cu = 1;
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess) return per_cu;

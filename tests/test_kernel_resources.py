@@ -11,7 +11,10 @@ SGPR file allows on MI355X.  Measured with a probe kernel of 256 threads,
 says 8); 96 -> 6 (the query says 7); with 80 VGPRs, 100 -> 6.  So each
 kernel's SGPR count is held to what its target occupancy allows:
   * decoder: 8 waves per SIMD (64 VGPRs) and next_free_sgpr <= 74;
-  * encoder: 5 waves per SIMD (96 VGPRs) and next_free_sgpr <= 100.
+  * encoder: two-wave workgroups at 3 waves per SIMD (168 VGPRs, six
+    workgroups per CU) and next_free_sgpr <= 100 (3 x 100 SGPRs per SIMD is
+    far below the limit measured above); six workgroups' LDS must fit the
+    CU's 160 KiB.
 """
 
 from __future__ import annotations
@@ -70,11 +73,11 @@ def test_persistent_decoder_fits_eight_waves(kernels):
         assert m["scratch"] == 0, (k, m)
 
 
-def test_persistent_encoder_fits_five_waves(kernels):
+def test_persistent_encoder_fits_three_waves(kernels):
     for k, m in pick(kernels, "compress_persistent_kernel").items():
         if "decompress" in k:
             continue
-        assert m["vgpr"] <= 96, (k, m)
+        assert m["vgpr"] <= 168, (k, m)
         assert m["sgpr"] <= 100, (k, m)
-        assert m["lds"] <= 32 * 1024, (k, m)
+        assert 6 * m["lds"] <= 160 * 1024, (k, m)
         assert m["scratch"] == 0, (k, m)
