@@ -454,9 +454,19 @@ __device__ __forceinline__ void lookback_publish(unsigned long long* state,
 // back over earlier tiles of the job 64 at a time until it meets one whose
 // inclusive prefix is published, publishes this tile's inclusive prefix and
 // returns the exclusive one (bytes of earlier tiles of the job).
+// lookback_first_addr: the word of the first window lookback_wait reads in
+// this lane (lanes outside the window get t's own word, which is ignored),
+// for a caller that issues that read early, ahead of other memory traffic.
+__device__ __forceinline__ const unsigned long long* lookback_first_addr(
+    const unsigned long long* state, uint32_t t, uint32_t tile) {
+    const uint32_t lane = __lane_id();
+    return (tile != 0 && lane < (tile < 64u ? tile : 64u)) ? &state[t - 1 - lane] : &state[t];
+}
+
 __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
                                   uint32_t tile, uint32_t total, uint32_t epoch,
-                                  uint32_t* err, uint32_t* host_ctl) {
+                                  uint32_t* err, uint32_t* host_ctl,
+                                  bool have_first = false, unsigned long long first = 0) {
     if (tile == 0) return 0;
     const int lane = __lane_id();
     const uint32_t tag_agg = epoch * 4u + 1u;
@@ -471,7 +481,12 @@ __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
             nwin == 64u ? ~0ull : ((1ull << nwin) - 1ull);
         unsigned long long w = 0, need = 0, incl = 0;
         for (uint32_t spins = 0;; ++spins) {
-            w = in_win ? load_relaxed(&state[pos - lane]) : 0ull;
+            if (have_first) {  // the caller's early read of this window
+                w = first;
+                have_first = false;
+            } else {
+                w = in_win ? load_relaxed(&state[pos - lane]) : 0ull;
+            }
             const uint32_t tag = (uint32_t)(w >> 32);
             incl = __ballot(in_win && tag == tag_inc);
             const unsigned long long ready =
@@ -946,6 +961,12 @@ __device__ __forceinline__ uint64_t enc_block_source(const Group& g, uint32_t ti
         .src_index;
 }
 
+// Sixteen zero words, the source of blocks that do not exist: every lane
+// then loads unconditionally.  (Loads under a branch make the compiler wait
+// for all outstanding memory operations at the next use of any earlier
+// load, which would tie the persistent encoder's polls to its prefetch.)
+__device__ __attribute__((aligned(16))) uint32_t g_zero_block[kBlockElems / 2];
+
 // This thread's block (zeros when it does not exist): four 16-byte loads.
 // A layer index outside [0, source_layers) is reported at once (the block is
 // then read from layer 0).
@@ -954,12 +975,13 @@ __device__ __forceinline__ void load_block_regs(const CompressParams& p, const T
                                                 uint32_t* d) {
     const bool ex = block_exists(g, c.tile, wave * 64 + lane);
     uint32_t bad = 0;
-    const g_u32x4* src = (const g_u32x4*)to_global(
-        job_of(p, c).in + (ex ? enc_block_source(g, c.tile, wave, lane, &bad) : 0));
+    const uint64_t off = ex ? enc_block_source(g, c.tile, wave, lane, &bad) : 0;
     if (bad) flag_error(p.error, p.host_ctl, kErrLayerIndex);
+    const g_u32x4* src = ex ? (const g_u32x4*)to_global(job_of(p, c).in + off)
+                            : (const g_u32x4*)to_global(&g_zero_block[0]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const u32x4 v = ex ? src[i] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v = src[i];
         d[4 * i + 0] = v.x;
         d[4 * i + 1] = v.y;
         d[4 * i + 2] = v.z;
@@ -1007,10 +1029,11 @@ __device__ __forceinline__ void load_block_from(const CompressParams& p, const T
         return;
     }
     const bool ex = block_exists(g, c.tile, wave * 64 + lane);
-    const g_u32x4* src = (const g_u32x4*)to_global(s.base + (ex ? (uint32_t)lane * kBlockElems : 0u));
+    const g_u32x4* src = ex ? (const g_u32x4*)to_global(s.base + (uint32_t)lane * kBlockElems)
+                            : (const g_u32x4*)to_global(&g_zero_block[0]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const u32x4 v = ex ? src[i] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v = src[i];
         d[4 * i + 0] = v.x;
         d[4 * i + 1] = v.y;
         d[4 * i + 2] = v.z;
@@ -1139,14 +1162,18 @@ constexpr float kFastLimit = 32766.0f;
 
 // Wave 0: the min/max keys over all tiles of the job (lane i polls tiles
 // i, i + 64, ...; all lanes end together).
+
+// `probe` (when `have_probe`) is an earlier read of lane's first word.
 __device__ __forceinline__ void job_keys(const CompressParams& p, uint32_t first_t,
                                          uint32_t tiles, int lane, uint32_t& kmin,
-                                         uint32_t& kmax) {
+                                         uint32_t& kmax, bool have_probe,
+                                         unsigned long long probe) {
     kmin = kKeyEmptyMin;
     kmax = kKeyEmptyMax;
     for (uint32_t i = (uint32_t)lane; i < tiles; i += 64u) {
         const unsigned long long* slot = &p.tile_minmax[first_t + i];
-        unsigned long long w = load_relaxed(slot);
+        unsigned long long w = have_probe && i < 64u ? probe : load_relaxed(slot);
+        have_probe = false;
         for (uint32_t spins = 0; (uint32_t)(w >> 32) != p.epoch; ++spins) {
             if (spins >= kSpinLimit) {
                 flag_error(p.error, p.host_ctl, kErrSpin);
@@ -1263,13 +1290,13 @@ __device__ __forceinline__ uint32_t block_rows(uint32_t* d, float recip, bool fa
     return o ? 32u - (uint32_t)__builtin_clz(o) : 0u;
 }
 
-// Three waves per SIMD (at most 168 VGPRs, no scratch).
+// Four waves per SIMD (at most 128 VGPRs, no scratch).
 //
-// Per tile: (a) wave 0 gathers the job's min/max and works out the bound
-// while wave 1 finishes the look-back of the tile staged one iteration
-// earlier; (d) that tile's payload out; (b) per 64-block half of each wave:
-// rows, rates, the wave scan, staging; then the tile scan, header and
-// aggregate out; (c) the next tile's keys out and the tile after it loading.
+// Per tile: the next tile starts loading; (a) wave 0 gathers the job's
+// min/max and works out the bound while wave 1 finishes the look-back of the
+// tile staged one iteration earlier; (d) that tile's payload out; (b) per
+// 64-block half of each wave: rows, rates, the wave scan, staging; then the
+// tile scan, header and aggregate out; (c) the next tile's keys out.
 //
 // Deferred stores: a tile's payload is staged in LDS at wave-relative
 // offsets and written out one iteration later, after the tile's look-back,
@@ -1287,7 +1314,7 @@ __device__ __forceinline__ uint32_t block_rows(uint32_t* d, float recip, bool fa
 // while all G workgroups are resident.
 template <int kQuant>
 __global__ __launch_bounds__(kEncThreads)
-__attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
+__attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
     CompressParams p) {
     __shared__ uint32_t s_wave[2][kEncWaves];
     __shared__ uint32_t s_min[kEncWaves], s_max[kEncWaves];
@@ -1307,7 +1334,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
     const bool fused = p.bound_mode == kBoundFused;
     bool pending = false;  // a tile's payload waits in the staging words
 
-    // Prologue: the first tile and its keys (published), the next one loading.
+    // Prologue: the first tile and its keys (published).
     TileCtx cur = tile_ctx(p, blockIdx.x, s_gfirst);
     uint32_t D0[16], D1[16], N0[16], N1[16];
     // Keys of the current tile's blocks: the published keys, except that a
@@ -1332,17 +1359,12 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         if (nan0) keys0 = kNanRateKeys;
         if (nan1) keys1 = kNanRateKeys;
         has_next = cur.t + G < p.total_tiles;
-        if (has_next) {
-            nxt = tile_ctx(p, cur.t + G, s_gfirst);
-            const Group& gn = p.groups[nxt.gi];
-            load_block_regs(p, nxt, gn, 2 * wave, lane, N0);
-            load_block_regs(p, nxt, gn, 2 * wave + 1, lane, N1);
-        }
+        if (has_next) nxt = tile_ctx(p, cur.t + G, s_gfirst);
     }
 
-    // One tile.  X holds this tile's values, Y the next tile's (loading since
-    // the previous iteration); the tile after that is loaded into X once X
-    // is no longer needed, and the next call swaps the roles (no copies).
+    // One tile.  X holds this tile's values; the next tile is loaded into Y
+    // (whose values were used up in the previous iteration), and the next
+    // call swaps the roles (no copies).
     uint32_t parity = 0;
     auto iteration = [&](uint32_t (&X0)[16], uint32_t (&X1)[16], uint32_t (&Y0)[16],
                          uint32_t (&Y1)[16]) -> bool {
@@ -1352,17 +1374,30 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         const Group& g = p.groups[cur.gi];
         const uint32_t blk0 = 128u * (uint32_t)wave + (uint32_t)lane;
 
-        // The tile loaded at c. (two ahead): its context and this wave's
-        // sources now, so that the scalar loads and divisions overlap the
-        // waits below.
-        const bool has_after = has_next && nxt.t + G < p.total_tiles;
-        TileCtx after = nxt;
-        WaveSource asrc0{nullptr}, asrc1{nullptr};
-        if (has_after) {
-            after = tile_ctx(p, nxt.t + G, s_gfirst);
-            const Group& ga = p.groups[after.gi];
-            asrc0 = wave_source(p, after, ga, 2 * wave);
-            asrc1 = wave_source(p, after, ga, 2 * wave + 1);
+        // First reads of a.'s waits (wave 0: the job's min/max words; wave
+        // 1: the pending tile's first look-back window), then the next tile's
+        // loads: loads and stores retire in order, so reads issued after the
+        // loads would wait for them, while these wait only for themselves.
+        // The next tile's values are needed at c.
+        // Every path issues one read and then eight loads, unconditionally
+        // (with a harmless address where there is nothing to read), so the
+        // wait for the read counts only the read.
+        const unsigned long long* paddr = &p.tile_state[cur.t];
+        if (wave == 0) {
+            if (fused)
+                paddr = &p.tile_minmax[cur.t - cur.tile +
+                                       min((uint32_t)lane, g.tiles_per_job - 1u)];
+        } else if (pending) {
+            const PendingTile& q = s_pend[parity ^ 1u];
+            paddr = lookback_first_addr(p.tile_state, q.t, q.tile);
+        }
+        const unsigned long long probe = load_relaxed(paddr);
+        {
+            const TileCtx& lc = has_next ? nxt : cur;  // cur: values unused
+            const Group& gl = p.groups[lc.gi];
+            load_block_from(p, lc, gl, wave_source(p, lc, gl, 2 * wave), 2 * wave, lane, Y0);
+            load_block_from(p, lc, gl, wave_source(p, lc, gl, 2 * wave + 1), 2 * wave + 1,
+                            lane, Y1);
         }
 
         // a. wave 0: the bound; wave 1: the pending tile's look-back.
@@ -1372,7 +1407,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
             uint32_t fast = 0;
             if (fused) {
                 uint32_t kmin, kmax;
-                job_keys(p, cur.t - cur.tile, g.tiles_per_job, lane, kmin, kmax);
+                job_keys(p, cur.t - cur.tile, g.tiles_per_job, lane, kmin, kmax, true, probe);
                 eb = relative_bound(eps, kmin, kmax);
                 const float jabs = fmaxf(fabsf(min_key_value(kmin)), fabsf(max_key_value(kmax)));
                 fast = jabs * (0.5f / eb) <= kFastLimit ? 1u : 0u;
@@ -1385,7 +1420,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         } else if (pending) {
             const PendingTile& q = s_pend[parity ^ 1u];
             const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                              p.epoch, p.error, p.host_ctl);
+                                              p.epoch, p.error, p.host_ctl, true, probe);
             if (lane == 0) {
                 s_prefix[parity] = pf;
                 if (q.last)
@@ -1405,6 +1440,22 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
             if (words)
                 copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[parity] + woff),
                              words, &s_stage[wave][0], lane);
+        }
+
+        // c. the next tile's keys and min/max, published early so that the
+        // exchanges of the next iteration, here and in the other workgroups
+        // holding tiles of its job, do not wait for them.
+        uint32_t nkeys0 = 0, nkeys1 = 0;
+        if (has_next) {
+            const Group& gn = p.groups[nxt.gi];
+            uint32_t nnan0, nnan1;
+            nkeys0 = block_keys(Y0, block_exists(gn, nxt.tile, (int)blk0), nnan0);
+            nkeys1 = block_keys(Y1, block_exists(gn, nxt.tile, (int)blk0 + 64), nnan1);
+            if (fused)
+                publish_keys2(p, nxt.t, min(nkeys0 >> 16, nkeys1 >> 16),
+                              max(nkeys0 & 0xFFFFu, nkeys1 & 0xFFFFu), s_min, s_max, wave, lane);
+            if (nnan0) nkeys0 = kNanRateKeys;
+            if (nnan1) nkeys1 = kNanRateKeys;
         }
 
         // b. per half: rows, rate, the wave's offsets, staging (cu:302-358:
@@ -1513,35 +1564,13 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         }
         pending = true;
 
-        // c. the next tile's keys and min/max (its loads were issued one
-        // iteration ago and complete here); this tile's values are no longer
-        // needed, so the tile after the next one starts loading into X --
-        // each load then has a whole iteration to arrive.
-        uint32_t nkeys0 = 0, nkeys1 = 0;
-        if (has_next) {
-            const Group& gn = p.groups[nxt.gi];
-            uint32_t nnan0, nnan1;
-            nkeys0 = block_keys(Y0, block_exists(gn, nxt.tile, (int)blk0), nnan0);
-            nkeys1 = block_keys(Y1, block_exists(gn, nxt.tile, (int)blk0 + 64), nnan1);
-            if (fused)
-                publish_keys2(p, nxt.t, min(nkeys0 >> 16, nkeys1 >> 16),
-                              max(nkeys0 & 0xFFFFu, nkeys1 & 0xFFFFu), s_min, s_max, wave, lane);
-            if (nnan0) nkeys0 = kNanRateKeys;
-            if (nnan1) nkeys1 = kNanRateKeys;
-            if (has_after) {
-                const Group& ga = p.groups[after.gi];
-                load_block_from(p, after, ga, asrc0, 2 * wave, lane, X0);
-                load_block_from(p, after, ga, asrc1, 2 * wave + 1, lane, X1);
-            }
-        }
-
         // f. advance
         if (!has_next) return false;
         cur = nxt;
         keys0 = nkeys0;
         keys1 = nkeys1;
         has_next = cur.t + G < p.total_tiles;
-        if (has_next) nxt = after.t == cur.t + G ? after : tile_ctx(p, cur.t + G, s_gfirst);
+        if (has_next) nxt = tile_ctx(p, cur.t + G, s_gfirst);
         return true;
     };
     for (;;) {
