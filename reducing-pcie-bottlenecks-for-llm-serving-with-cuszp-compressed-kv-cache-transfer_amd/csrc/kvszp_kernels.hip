@@ -967,13 +967,13 @@ __device__ __forceinline__ uint64_t enc_block_source(const Group& g, uint32_t ti
 // load, which would tie the persistent encoder's polls to its prefetch.)
 __device__ __attribute__((aligned(16))) uint32_t g_zero_block[kBlockElems / 2];
 
-// This thread's block (zeros when it does not exist): four 16-byte loads.
-// A layer index outside [0, source_layers) is reported at once (the block is
-// then read from layer 0).
+// This thread's block (zeros when it does not exist, or when `live` is
+// false): four 16-byte loads.  A layer index outside [0, source_layers) is
+// reported at once (the block is then read from layer 0).
 __device__ __forceinline__ void load_block_regs(const CompressParams& p, const TileCtx& c,
                                                 const Group& g, int wave, int lane,
-                                                uint32_t* d) {
-    const bool ex = block_exists(g, c.tile, wave * 64 + lane);
+                                                uint32_t* d, bool live = true) {
+    const bool ex = live && block_exists(g, c.tile, wave * 64 + lane);
     uint32_t bad = 0;
     const uint64_t off = ex ? enc_block_source(g, c.tile, wave, lane, &bad) : 0;
     if (bad) flag_error(p.error, p.host_ctl, kErrLayerIndex);
@@ -1020,15 +1020,16 @@ __device__ __forceinline__ WaveSource wave_source(const CompressParams& p, const
     return s;
 }
 
-// This thread's block from a WaveSource (zeros when it does not exist).
+// This thread's block from a WaveSource (zeros when it does not exist, or
+// when `live` is false).
 __device__ __forceinline__ void load_block_from(const CompressParams& p, const TileCtx& c,
                                                 const Group& g, WaveSource s, int wave,
-                                                int lane, uint32_t* d) {
+                                                int lane, uint32_t* d, bool live) {
     if (s.base == nullptr) {
-        load_block_regs(p, c, g, wave, lane, d);
+        load_block_regs(p, c, g, wave, lane, d, live);
         return;
     }
-    const bool ex = block_exists(g, c.tile, wave * 64 + lane);
+    const bool ex = live && block_exists(g, c.tile, wave * 64 + lane);
     const g_u32x4* src = ex ? (const g_u32x4*)to_global(s.base + (uint32_t)lane * kBlockElems)
                             : (const g_u32x4*)to_global(&g_zero_block[0]);
 #pragma unroll
@@ -1380,8 +1381,8 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
         // loads would wait for them, while these wait only for themselves.
         // The next tile's values are needed at c.
         // Every path issues one read and then eight loads, unconditionally
-        // (with a harmless address where there is nothing to read), so the
-        // wait for the read counts only the read.
+        // (from a harmless address or the zero block where there is nothing
+        // to read), so the wait for the read counts only the read.
         const unsigned long long* paddr = &p.tile_state[cur.t];
         if (wave == 0) {
             if (fused)
@@ -1393,11 +1394,14 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
         }
         const unsigned long long probe = load_relaxed(paddr);
         {
-            const TileCtx& lc = has_next ? nxt : cur;  // cur: values unused
+            // Without a next tile the loads read the zero block (values
+            // unused), so that the loads are the same on every path.
+            const TileCtx& lc = has_next ? nxt : cur;
             const Group& gl = p.groups[lc.gi];
-            load_block_from(p, lc, gl, wave_source(p, lc, gl, 2 * wave), 2 * wave, lane, Y0);
+            load_block_from(p, lc, gl, wave_source(p, lc, gl, 2 * wave), 2 * wave, lane, Y0,
+                            has_next);
             load_block_from(p, lc, gl, wave_source(p, lc, gl, 2 * wave + 1), 2 * wave + 1,
-                            lane, Y1);
+                            lane, Y1, has_next);
         }
 
         // a. wave 0: the bound; wave 1: the pending tile's look-back.
