@@ -1293,11 +1293,12 @@ __device__ __forceinline__ uint32_t block_rows(uint32_t* d, float recip, bool fa
 
 // Four waves per SIMD (at most 128 VGPRs, no scratch).
 //
-// Per tile: the next tile starts loading; (a) wave 0 gathers the job's
-// min/max and works out the bound while wave 1 finishes the look-back of the
-// tile staged one iteration earlier; (d) that tile's payload out; (b) per
-// 64-block half of each wave: rows, rates, the wave scan, staging; then the
-// tile scan, header and aggregate out; (c) the next tile's keys out.
+// Per tile: the next tile starts loading; (c) its keys; (a) wave 0 gathers
+// the job's min/max and works out the bound while wave 1 finishes the
+// look-back of the tile staged one iteration earlier; the next tile's keys
+// out; (d) the staged tile's payload out; (b) per 64-block half of each
+// wave: rows, rates, the wave scan, staging; then the tile scan, header and
+// aggregate out.
 //
 // Deferred stores: a tile's payload is staged in LDS at wave-relative
 // offsets and written out one iteration later, after the tile's look-back,
@@ -1361,6 +1362,7 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
         if (nan1) keys1 = kNanRateKeys;
         has_next = cur.t + G < p.total_tiles;
         if (has_next) nxt = tile_ctx(p, cur.t + G, s_gfirst);
+        __syncthreads();  // thread 0 has read s_min/s_max before c. rewrites them
     }
 
     // One tile.  X holds this tile's values; the next tile is loaded into Y
@@ -1404,6 +1406,26 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
                             lane, Y1, has_next);
         }
 
+        // c. the next tile's keys, while the reads above are in flight; each
+        // wave's min/max goes to LDS now and the tile's word out after a.'s
+        // barrier, early in the iteration, so that the exchanges of the next
+        // iteration, here and in the other workgroups holding tiles of its
+        // job, do not wait for it.
+        uint32_t nkeys0 = 0, nkeys1 = 0, nnan0 = 0, nnan1 = 0;
+        if (has_next) {
+            const Group& gn = p.groups[nxt.gi];
+            nkeys0 = block_keys(Y0, block_exists(gn, nxt.tile, (int)blk0), nnan0);
+            nkeys1 = block_keys(Y1, block_exists(gn, nxt.tile, (int)blk0 + 64), nnan1);
+            if (fused) {
+                const uint32_t kmin = wave_min(min(nkeys0 >> 16, nkeys1 >> 16));
+                const uint32_t kmax = wave_max(max(nkeys0 & 0xFFFFu, nkeys1 & 0xFFFFu));
+                if (lane == 0) {
+                    s_min[wave] = kmin;
+                    s_max[wave] = kmax;
+                }
+            }
+        }
+
         // a. wave 0: the bound; wave 1: the pending tile's look-back.
         if (wave == 0) {
             const float eps = job_of(p, cur).eps;
@@ -1436,6 +1458,15 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
             }
         }
         __syncthreads();
+        if (has_next) {
+            if (fused && tid == 0) {
+                const uint32_t kmin = min(s_min[0], s_min[1]), kmax = max(s_max[0], s_max[1]);
+                store_relaxed(&p.tile_minmax[nxt.t],
+                              ((unsigned long long)p.epoch << 32) | (kmin << 16) | kmax);
+            }
+            if (nnan0) nkeys0 = kNanRateKeys;
+            if (nnan1) nkeys1 = kNanRateKeys;
+        }
 
         // d. the pending tile's payload out (frees the staging words)
         if (pending) {
@@ -1444,22 +1475,6 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
             if (words)
                 copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[parity] + woff),
                              words, &s_stage[wave][0], lane);
-        }
-
-        // c. the next tile's keys and min/max, published early so that the
-        // exchanges of the next iteration, here and in the other workgroups
-        // holding tiles of its job, do not wait for them.
-        uint32_t nkeys0 = 0, nkeys1 = 0;
-        if (has_next) {
-            const Group& gn = p.groups[nxt.gi];
-            uint32_t nnan0, nnan1;
-            nkeys0 = block_keys(Y0, block_exists(gn, nxt.tile, (int)blk0), nnan0);
-            nkeys1 = block_keys(Y1, block_exists(gn, nxt.tile, (int)blk0 + 64), nnan1);
-            if (fused)
-                publish_keys2(p, nxt.t, min(nkeys0 >> 16, nkeys1 >> 16),
-                              max(nkeys0 & 0xFFFFu, nkeys1 & 0xFFFFu), s_min, s_max, wave, lane);
-            if (nnan0) nkeys0 = kNanRateKeys;
-            if (nnan1) nkeys1 = kNanRateKeys;
         }
 
         // b. per half: rows, rate, the wave's offsets, staging (cu:302-358:
