@@ -593,6 +593,10 @@ class KVPageCodec:
             else:
                 key = (mode,)
             grouped.setdefault(key, []).append(item)
+        # Layer groups that scatter into full pages with the same page shape
+        # are restored by one grouped launch (the reference issues one
+        # indexed-scatter call per group; the values written are the same).
+        indexed = []
         for key, items in grouped.items():
             mode = str(key[0])
             compressor = self.compressors.get(mode)
@@ -605,14 +609,8 @@ class KVPageCodec:
             started = time.perf_counter()
             idx = self.fixed_bf16_indexed_destinations(items)
             if idx is not None:
-                outputs, index, prefix, src_layers, epl = idx
-                ok = compressor.decompress_batch_fixed_bf16_indexed_scatter(
-                    [it[2] for it in items], [it[1].compressed_size for it in items],
-                    outputs, index, prefix, src_layers, epl,
-                    [it[1].actual_error_bound for it in items])
+                indexed.append((compressor, items, idx))
                 timings.gpu_decode_seconds += time.perf_counter() - started
-                if not ok:
-                    raise RuntimeError("cuSZp failed to indexed-scatter a KV batch")
                 continue
             direct = self.fixed_bf16_direct_destinations(items)
             if direct is not None:
@@ -638,7 +636,40 @@ class KVPageCodec:
                 restored = storage[offset:offset + seg.compressed_numel]
                 offset += seg.compressed_numel
                 timings.add(self.decode_segment(gpu_block_id, seg, payload_gpu, restored))
+        if indexed:
+            started = time.perf_counter()
+            self.restore_indexed_groups(indexed)
+            timings.gpu_decode_seconds += time.perf_counter() - started
         return timings
+
+    @staticmethod
+    def restore_indexed_groups(indexed) -> None:
+        """Indexed-scatter restores: one launch for all groups sharing the
+        compressor and page geometry (prefix, source layers, elements per
+        layer), else one call per group as in :1899-1908."""
+        by_shape: dict[tuple, list] = {}
+        for compressor, items, idx in indexed:
+            _, _, prefix, src_layers, epl = idx
+            by_shape.setdefault((id(compressor), prefix, src_layers, epl), []).append(
+                (compressor, items, idx))
+        for (_, prefix, src_layers, epl), groups in by_shape.items():
+            compressor = groups[0][0]
+            streams, sizes, outputs, bounds, indices, counts = [], [], [], [], [], []
+            for _, items, idx in groups:
+                streams += [it[2] for it in items]
+                sizes += [it[1].compressed_size for it in items]
+                bounds += [it[1].actual_error_bound for it in items]
+                outputs += idx[0]
+                indices.append(idx[1])
+                counts.append(len(items))
+            if len(groups) == 1:
+                ok = compressor.decompress_batch_fixed_bf16_indexed_scatter(
+                    streams, sizes, outputs, indices[0], prefix, src_layers, epl, bounds)
+            else:
+                ok = compressor.decompress_batch_fixed_bf16_indexed_scatter_groups(
+                    streams, sizes, outputs, indices, counts, prefix, src_layers, epl, bounds)
+            if not ok:
+                raise RuntimeError("cuSZp failed to indexed-scatter a KV batch")
 
     def decode_segment(self, gpu_block_id: int, segment: EncodedSegment,
                        payload_gpu: torch.Tensor,
