@@ -235,9 +235,9 @@ def _pmc_per_dispatch(run_dir: str, counter: str) -> dict:
     for did in sorted(per):
         name = names[did]
         if "kvszp::" in name and "decompress" in name:
-            kind = "decompress_kernel"   # decompress_kernel / decompress_pipelined_kernel
+            kind = "decompress_kernel"   # decompress_kernel / decompress_persistent_kernel
         elif "kvszp::" in name and "compress" in name and "minmax" not in name:
-            kind = "compress_kernel"     # compress_kernel / compress_pipelined_kernel
+            kind = "compress_kernel"     # compress_kernel / compress_persistent_kernel
         elif "copyBuffer" in name:
             kind = "copy"
         else:

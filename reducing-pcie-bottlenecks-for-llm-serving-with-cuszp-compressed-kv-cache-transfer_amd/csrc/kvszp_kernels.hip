@@ -2,19 +2,22 @@
 // KV-page codec.
 //
 // Reference semantics: integration/cuszp_wrapper/cuszp_batched_fixed.cu
-//   quantizer            :10-25   -> quantize()
-//   rate                 :27-31   -> block_rate()
+//   quantizer            :10-25   -> quantize(), build_rows_signhi()
+//   rate                 :27-31   -> bit length of the OR of |q| (the rows)
 //   layer gather         :33-50   -> LayerCursor / map_index()
 //   relative bound       :55-133  -> fused min/max exchange (compress) or
 //                                    minmax_kernel (pre-pass)
-//   encoder              :135-359 -> compress_kernel
-//   decoder              :361-627 -> decompress_kernel
+//   encoder              :135-359 -> compress_persistent_kernel, compress_kernel
+//   decoder              :361-627 -> decompress_persistent_kernel,
+//                                    decompress_kernel
 //
-// Schedule (not the reference's): one workgroup of 256 threads per tile of
-// 256 blocks, ONE THREAD PER 32-ELEMENT BLOCK.  A thread loads its block with
-// four 16-byte loads, quantizes in registers, and builds the sign and plane
-// words with a register bit-matrix transpose (kvszp_bits.h) instead of the
-// reference's per-bit loops.  Block offsets come from a workgroup scan plus a
+// Schedule (not the reference's): tiles of 256 blocks.  The one-workgroup-
+// per-tile kernels use 256 threads, ONE THREAD PER 32-ELEMENT BLOCK; the
+// persistent encoder uses two waves with two blocks per thread, the
+// persistent decoder four waves with one, each walking many tiles.  A thread
+// loads its blocks with 16-byte loads, quantizes in registers, and builds the
+// sign and plane words with a register bit-matrix transpose (kvszp_bits.h)
+// instead of the reference's per-bit loops.  Block offsets come from a workgroup scan plus a
 // decoupled look-back across the tiles of a job.  Cross-workgroup state is a
 // single 64-bit word per tile holding {epoch tag, status, value}, read and
 // written with relaxed agent-scope atomics (these bypass the per-XCD L2), so
