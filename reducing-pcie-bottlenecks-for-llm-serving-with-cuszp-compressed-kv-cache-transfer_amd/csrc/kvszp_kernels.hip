@@ -3,7 +3,8 @@
 //
 // Reference semantics: integration/cuszp_wrapper/cuszp_batched_fixed.cu
 //   quantizer            :10-25   -> quantize(), build_rows_signhi()
-//   rate                 :27-31   -> bit length of the OR of |q| (the rows)
+//   rate                 :27-31   -> rate_from_keys(), rate_by_quantizing(),
+//                                    OR of |q| (compress_kernel)
 //   layer gather         :33-50   -> LayerCursor / map_index()
 //   relative bound       :55-133  -> fused min/max exchange (compress) or
 //                                    minmax_kernel (pre-pass)
@@ -1101,6 +1102,32 @@ __device__ __forceinline__ uint32_t block_keys(const uint32_t* d, bool exists,
 // NaN: they mark the block so that its wave takes the exact quantizer.
 constexpr uint32_t kNanRateKeys = (0x007Fu << 16) | 0xFF80u;
 
+// Rate of a block from its keys, for a block whose values all satisfy
+// |x * recip| <= kFastLimit and that holds no NaN: the quantizer is monotone
+// there, so the largest |q| is that of the block's smallest or largest value.
+template <int kQuant>
+__device__ __forceinline__ uint32_t rate_from_keys(uint32_t keys, float recip) {
+    const uint32_t m = max(magnitude(quantize<kQuant>(key_value(keys >> 16), recip)),
+                           magnitude(quantize<kQuant>(key_value(keys & 0xFFFFu), recip)));
+    return m ? 32u - (uint32_t)__builtin_clz(m) : 0u;
+}
+
+// Rate of a block by quantizing every value (NaN, saturation, wrap).  Each
+// value's reciprocal passes through an empty asm that takes the running OR
+// as an input, so the values are done one after the other (this rare path
+// then needs few registers).
+template <int kQuant>
+__device__ __forceinline__ uint32_t rate_by_quantizing(const uint32_t* d, float recip) {
+    uint32_t orv = 0;
+#pragma unroll
+    for (int v = 0; v < kBlockElems; ++v) {
+        float r = recip;
+        asm volatile("" : "+v"(r) : "v"(orv));
+        orv |= magnitude(quant_elem<kQuant, true>(d, v, kBlockElems, r));
+    }
+    return orv ? 32u - (uint32_t)__builtin_clz(orv) : 0u;
+}
+
 // a * b + c for a, b < 2^24 as one instruction (the compiler otherwise
 // expands s * 0x8001 for a 0/1 value s into an arithmetic shift and an AND).
 __device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
@@ -1215,17 +1242,6 @@ __device__ __forceinline__ void publish_keys2(const CompressParams& p, uint32_t 
     }
 }
 
-// Rate of a block from its sign-high field rows (before the transpose): the
-// OR of the rows has the bit length of the largest |q| in its low 15 bits
-// of either half.
-__device__ __forceinline__ uint32_t rate_of_rows(const uint32_t* P) {
-    uint32_t o = 0;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) o |= P[k];
-    const uint32_t m = (o | (o >> 16)) & 0x7FFFu;
-    return m ? 32u - (uint32_t)__builtin_clz(m) : 0u;
-}
-
 // A wave's payload staged in LDS: the block is words [off, off + count) of
 // the wave's payload.  The stream words are the transposed rows P:
 // w_j = P[j] (kSignHi false), or w_0 = P[15] and w_j = P[j - 1] (sign-high
@@ -1277,24 +1293,7 @@ __device__ __forceinline__ void stage_high_words(const uint32_t* P, uint32_t cou
     __asm__ volatile("" ::: "memory");
 }
 
-// Rows of one block (cu:180-231) and its rate.  Fast path: sign-high rows
-// (sign << 15) | |q|, whose transpose gives planes 0..14 then the sign word.
-// Otherwise the exact quantizer's low fields ((|q| << 1) | sign) & 0xFFFF,
-// whose transpose gives words 0..15 in stream order.  Either way the rate is
-// the bit length of the OR of |q|.
-template <int kQuant>
-__device__ __forceinline__ uint32_t block_rows(uint32_t* d, float recip, bool fast,
-                                               uint32_t* P) {
-    if (fast) {
-        build_rows_signhi<kQuant>(d, recip, P);
-        return rate_of_rows(P);
-    }
-    uint32_t o = 0;
-    build_rows_lo_chained<kQuant>(d, recip, P, o);
-    return o ? 32u - (uint32_t)__builtin_clz(o) : 0u;
-}
-
-// Four waves per SIMD (at most 128 VGPRs, no scratch).
+// Three waves per SIMD (at most 168 VGPRs, no scratch).
 //
 // Per tile: the next tile starts loading; (c) its keys; (a) wave 0 gathers
 // the job's min/max and works out the bound while wave 1 finishes the
@@ -1319,7 +1318,7 @@ __device__ __forceinline__ uint32_t block_rows(uint32_t* d, float recip, bool fa
 // while all G workgroups are resident.
 template <int kQuant>
 __global__ __launch_bounds__(kEncThreads)
-__attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
+__attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
     CompressParams p) {
     __shared__ uint32_t s_wave[2][kEncWaves];
     __shared__ uint32_t s_min[kEncWaves], s_max[kEncWaves];
@@ -1380,14 +1379,14 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
         const Group& g = p.groups[cur.gi];
         const uint32_t blk0 = 128u * (uint32_t)wave + (uint32_t)lane;
 
-        // First reads of a.'s waits (wave 0: the job's min/max words; wave
-        // 1: the pending tile's first look-back window), then the next tile's
-        // loads: loads and stores retire in order, so reads issued after the
-        // loads would wait for them, while these wait only for themselves.
-        // The next tile's values are needed at c.
-        // Every path issues one read and then eight loads, unconditionally
-        // (from a harmless address or the zero block where there is nothing
-        // to read), so the wait for the read counts only the read.
+        // First reads of the waits (wave 0: the job's min/max words for a.;
+        // wave 1: the pending tile's first look-back window), then the next
+        // tile's loads: loads and stores retire in order, so reads issued
+        // after the loads would wait for them, while these wait only for
+        // themselves.  The next tile's values are needed at c.  Every path
+        // issues one read and then eight loads, unconditionally (from a
+        // harmless address or the zero block where there is nothing to
+        // read), so the wait for the read counts only the read.
         const unsigned long long* paddr = &p.tile_state[cur.t];
         if (wave == 0) {
             if (fused)
@@ -1429,7 +1428,8 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
             }
         }
 
-        // a. wave 0: the bound; wave 1: the pending tile's look-back.
+        // a. wave 0: the bound (one barrier hands it over; thread 0 then
+        // publishes the next tile's min/max).
         if (wave == 0) {
             const float eps = job_of(p, cur).eps;
             float eb = eps;
@@ -1446,19 +1446,6 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
                 s_bnd[parity][1] = 0.5f / eb;  // cu:166, IEEE division
                 s_fast[parity] = fast;
             }
-        } else if (pending) {
-            const PendingTile& q = s_pend[parity ^ 1u];
-            const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                              p.epoch, p.error, p.host_ctl, true, probe);
-            if (lane == 0) {
-                s_prefix[parity] = pf;
-                if (q.last)
-                    __hip_atomic_store(&p.host_sizes[q.job], q.R + pf + q.total,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                if (q.first)
-                    __hip_atomic_store(&p.host_bounds[q.job], q.eb, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_SYSTEM);
-            }
         }
         __syncthreads();
         if (has_next) {
@@ -1471,28 +1458,21 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
             if (nnan1) nkeys1 = kNanRateKeys;
         }
 
-        // d. the pending tile's payload out (frees the staging words)
-        if (pending) {
-            const PendingTile& q = s_pend[parity ^ 1u];
-            const uint32_t woff = s_pwave[wave][0], words = s_pwave[wave][1];
-            if (words)
-                copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[parity] + woff),
-                             words, &s_stage[wave][0], lane);
-        }
-
-        // b. per half: rows, rate, the wave's offsets, staging (cu:302-358:
-        // sign word, then `rate` plane words).  Fast path when no block of
-        // the wave holds a NaN and every |x * recip| is at most kFastLimit,
-        // known for the whole job from its min/max or else from the keys.
+        // b. rates (cu:212-231) and the wave's offsets.  Fast path when no
+        // block of the wave holds a NaN and every |x * recip| is at most
+        // kFastLimit (known for the whole job from its min/max, or else from
+        // the keys): the quantizer is monotone there, so a block's largest
+        // |q| is at its smallest or largest value and the rate comes from
+        // the keys alone.  Otherwise every value is quantized.
         const float eb = s_bnd[parity][0];
         const float recip = s_bnd[parity][1];
+        const bool ex0 = block_exists(g, cur.tile, (int)blk0);
+        const bool ex1 = block_exists(g, cur.tile, (int)blk0 + 64);
         bool fast_w = false;
         if (__ballot(keys0 == kNanRateKeys || keys1 == kNanRateKeys) == 0ull) {
             if (s_fast[parity] != 0) {
                 fast_w = true;
             } else {
-                const bool ex0 = block_exists(g, cur.tile, (int)blk0);
-                const bool ex1 = block_exists(g, cur.tile, (int)blk0 + 64);
                 const float bmax0 = fmaxf(fabsf(key_value(keys0 >> 16)), fabsf(key_value(keys0 & 0xFFFFu)));
                 const float bmax1 = fmaxf(fabsf(key_value(keys1 >> 16)), fabsf(key_value(keys1 & 0xFFFFu)));
                 const bool ok = (!ex0 || bmax0 * recip <= kFastLimit) &&
@@ -1500,50 +1480,32 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
                 fast_w = __ballot(!ok) == 0ull;
             }
         }
-        // A wave whose payload would not fit the staging words (rates far
-        // above 15 throughout) stages no more and tells the host, which
-        // encodes the whole launch again with the one-workgroup-per-tile
-        // kernel; the rest of this launch carries on normally.
-        uint32_t wave_bytes = 0;
-        bool overflow = false;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            uint32_t (&X)[16] = h ? X1 : X0;
-            uint32_t P[16];
-            const uint32_t rate = block_rows<kQuant>(X, recip, fast_w, P);
-            const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
-            const uint32_t count = rate ? rate + 1u : 0u;
-            const uint32_t incl = wave_inclusive_scan(bytes, lane);
-            const uint32_t half_bytes = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-            const uint32_t rmax = wave_max(rate);
-            s_rate[parity][blk0 + 64u * h] = (uint8_t)rate;
-            const uint32_t off = (wave_bytes + incl - bytes) >> 2;  // words
-            wave_bytes += half_bytes;
-            overflow = overflow || (wave_bytes >> 2) + 16u > (uint32_t)kEncStageWords;
-            if (!overflow && rmax != 0) {
-                transpose16x2(P);
-                const uint32_t cmax = rmax < 15u ? rmax + 1u : 16u;
-                if (fast_w) {
-                    stage_payload<true>(P, count, off, cmax, &s_stage[wave][0]);
-                } else {
-                    stage_payload<false>(P, count < 16u ? count : 16u, off, cmax,
-                                         &s_stage[wave][0]);
-                    if (rmax > 15u) {
-                        // Words 16..31 (rates above 15, rare): high fields,
-                        // staged exactly.
-                        build_rows_hi_chained<kQuant>(X, recip, P);
-                        transpose16x2(P);
-                        stage_high_words(P, count, off, &s_stage[wave][0]);
-                    }
-                }
-            }
+        uint32_t rate0 = 0, rate1 = 0;
+        if (fast_w) {
+            if (ex0) rate0 = rate_from_keys<kQuant>(keys0, recip);
+            if (ex1) rate1 = rate_from_keys<kQuant>(keys1, recip);
+        } else {
+            rate0 = rate_by_quantizing<kQuant>(X0, recip);  // absent blocks are zeros
+            rate1 = rate_by_quantizing<kQuant>(X1, recip);
         }
-        if (overflow && lane == 0)
-            __hip_atomic_store(&p.host_ctl[kHostOverflow], p.seq, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_SYSTEM);
+        const uint32_t bytes0 = rate0 ? 4u + 4u * rate0 : 0u;
+        const uint32_t bytes1 = rate1 ? 4u + 4u * rate1 : 0u;
+        const uint32_t incl0 = wave_inclusive_scan(bytes0, lane);
+        const uint32_t incl1 = wave_inclusive_scan(bytes1, lane);
+        const uint32_t half0 = (uint32_t)__builtin_amdgcn_readlane((int)incl0, 63);
+        const uint32_t half1 = (uint32_t)__builtin_amdgcn_readlane((int)incl1, 63);
+        const uint32_t rmax0 = wave_max(rate0), rmax1 = wave_max(rate1);
+        const uint32_t wave_bytes = half0 + half1;
+        s_rate[parity][blk0] = (uint8_t)rate0;
+        s_rate[parity][blk0 + 64] = (uint8_t)rate1;
+        // Staging slot of each block: word offset in the wave's payload (low
+        // half) and word count (high half).
+        const uint32_t slot0 = ((incl0 - bytes0) >> 2) | ((rate0 ? rate0 + 1u : 0u) << 16);
+        const uint32_t slot1 = ((half0 + incl1 - bytes1) >> 2) | ((rate1 ? rate1 + 1u : 0u) << 16);
 
         // Tile scan (the barrier), header bytes (padding zeroed by the last
-        // tile), aggregate out.
+        // tile), aggregate out -- before the rows, so that the look-backs of
+        // the tiles after this one find it early.
         if (lane == 0) s_wave[parity][wave] = wave_bytes;
         __syncthreads();
         const uint32_t wb0 = s_wave[parity][0];
@@ -1564,6 +1526,78 @@ __attribute__((amdgpu_waves_per_eu(4, 4))) void compress_persistent_kernel(
                 *to_global(reinterpret_cast<uint32_t*>(job_of(p, cur).out + off)) = 0u;
         }
         if (wave == 0) lookback_publish(p.tile_state, cur.t, cur.tile, total, p.epoch);
+
+        // The pending tile's look-back (wave 1; its first read went out with
+        // the loads, and its predecessors published their aggregates early
+        // in the previous iteration); one barrier hands the prefix over.
+        if (wave == 1 && pending) {
+            const PendingTile& q = s_pend[parity ^ 1u];
+            const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
+                                              p.epoch, p.error, p.host_ctl, true, probe);
+            if (lane == 0) {
+                s_prefix[parity] = pf;
+                if (q.last)
+                    __hip_atomic_store(&p.host_sizes[q.job], q.R + pf + q.total,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (q.first)
+                    __hip_atomic_store(&p.host_bounds[q.job], q.eb, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+        __syncthreads();
+
+        // d. the pending tile's payload out (frees the staging words)
+        if (pending) {
+            const PendingTile& q = s_pend[parity ^ 1u];
+            const uint32_t woff = s_pwave[wave][0], words = s_pwave[wave][1];
+            if (words)
+                copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[parity] + woff),
+                             words, &s_stage[wave][0], lane);
+        }
+
+        // e. rows (cu:180-231) and staging (cu:302-358: sign word, then
+        // `rate` plane words).  Fast path: sign-high rows (sign << 15) | |q|,
+        // whose transpose gives planes 0..14 then the sign word; otherwise
+        // the exact quantizer's low fields ((|q| << 1) | sign) & 0xFFFF,
+        // whose transpose gives words 0..15 in stream order, and for rates
+        // above 15 the high fields |q| >> 15 (words 16..31), staged exactly.
+        // A wave whose payload would not fit the staging words (rates far
+        // above 15 throughout) stages nothing and tells the host, which
+        // encodes the whole launch again with the one-workgroup-per-tile
+        // kernel; the rest of this launch carries on normally.
+        const bool overflow = (wave_bytes >> 2) + 16u > (uint32_t)kEncStageWords;
+        if (overflow) {
+            if (lane == 0)
+                __hip_atomic_store(&p.host_ctl[kHostOverflow], p.seq, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t (&X)[16] = h ? X1 : X0;
+                const uint32_t rmax = h ? rmax1 : rmax0;
+                const uint32_t slot = h ? slot1 : slot0;
+                const uint32_t off = slot & 0xFFFFu, count = slot >> 16;
+                if (rmax == 0) continue;
+                uint32_t P[16];
+                const uint32_t cmax = rmax < 15u ? rmax + 1u : 16u;
+                if (fast_w) {
+                    build_rows_signhi<kQuant>(X, recip, P);
+                    transpose16x2(P);
+                    stage_payload<true>(P, count, off, cmax, &s_stage[wave][0]);
+                } else {
+                    uint32_t orv = 0;
+                    build_rows_lo_chained<kQuant>(X, recip, P, orv);
+                    transpose16x2(P);
+                    stage_payload<false>(P, count < 16u ? count : 16u, off, cmax,
+                                         &s_stage[wave][0]);
+                    if (rmax > 15u) {
+                        build_rows_hi_chained<kQuant>(X, recip, P);
+                        transpose16x2(P);
+                        stage_high_words(P, count, off, &s_stage[wave][0]);
+                    }
+                }
+            }
+        }
         if (lane == 0) {
             s_pwave[wave][0] = wave_off;
             s_pwave[wave][1] = overflow ? 0u : wave_bytes >> 2;

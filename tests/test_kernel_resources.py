@@ -11,9 +11,9 @@ SGPR file allows on MI355X.  Measured with a probe kernel of 256 threads,
 says 8); 96 -> 6 (the query says 7); with 80 VGPRs, 100 -> 6.  So each
 kernel's SGPR count is held to what its target occupancy allows:
   * decoder: 8 waves per SIMD (64 VGPRs) and next_free_sgpr <= 74;
-  * encoder: two-wave workgroups at 4 waves per SIMD (128 VGPRs, eight
-    workgroups per CU) and next_free_sgpr <= 100 (4 x 100 SGPRs per SIMD is
-    below the limit measured above); eight workgroups' LDS must fit the
+  * encoder: two-wave workgroups at 3 waves per SIMD (168 VGPRs, six
+    workgroups per CU) and next_free_sgpr <= 100 (3 x 100 SGPRs per SIMD is
+    far below the limit measured above); six workgroups' LDS must fit the
     CU's 160 KiB.
 """
 
@@ -73,11 +73,11 @@ def test_persistent_decoder_fits_eight_waves(kernels):
         assert m["scratch"] == 0, (k, m)
 
 
-def test_persistent_encoder_fits_four_waves(kernels):
+def test_persistent_encoder_fits_three_waves(kernels):
     for k, m in pick(kernels, "compress_persistent_kernel").items():
         if "decompress" in k:
             continue
-        assert m["vgpr"] <= 128, (k, m)
+        assert m["vgpr"] <= 168, (k, m)
         assert m["sgpr"] <= 100, (k, m)
-        assert 8 * m["lds"] <= 160 * 1024, (k, m)
+        assert 6 * m["lds"] <= 160 * 1024, (k, m)
         assert m["scratch"] == 0, (k, m)
