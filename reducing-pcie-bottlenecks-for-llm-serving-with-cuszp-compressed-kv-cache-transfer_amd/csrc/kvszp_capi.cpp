@@ -564,6 +564,27 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     if (job != batch) return fail(KVSZP_EINVAL, "group sizes do not cover the batch");
     if (total_tiles > kMaxTiles) return fail(KVSZP_EINVAL, "batch too large for one launch");
 
+    // Persistent decoder: per-group tile weights (BF16 output plus the
+    // group's average payload per tile), so that workgroups holding tiles of
+    // a high-rate group get fewer of them.  Kernel arguments only: the table
+    // keeps its size.
+    {
+        uint64_t before = 0;
+        size_t j = 0;
+        for (size_t gi = 0; gi < specs.size(); ++gi) {
+            const GroupSpec& spec = specs[gi];
+            const Group& g = p.groups[gi];
+            uint64_t payload = 0;
+            for (uint32_t k = 0; k < spec.jobs; ++k, ++j) payload += sizes[j] - g.header_bytes;
+            const uint64_t tiles = (uint64_t)g.tiles_per_job * spec.jobs;
+            const uint64_t w = (2 * spec.n * spec.jobs + payload + tiles / 2) / tiles;
+            p.tile_weight[gi] = (uint32_t)std::max<uint64_t>(w, 1);
+            p.weight_before[gi] = before;
+            before += tiles * p.tile_weight[gi];
+        }
+        p.total_weight = before;
+    }
+
     // Packed table: jobs, then (kDstMulti) the destination pointers.
     const size_t jobs_bytes = (batch * sizeof(DecompressJob) + 255) & ~(size_t)255;
     std::vector<char> table(jobs_bytes + dest_table.size() * sizeof(uint16_t*));

@@ -135,6 +135,13 @@ struct DecompressParams {
     int aligned16;                    // every destination base 16B aligned
     uint64_t dests_per_page;
     uint64_t elements_per_dest;
+    // Persistent decoder runs balanced by bytes moved: each tile of group
+    // g weighs tile_weight[g] (its BF16 output plus the group's average
+    // payload per tile), weight_before[g] is the weight of the tiles before
+    // the group, total_weight that of all tiles; 0 = equal tile counts.
+    uint64_t total_weight;
+    uint64_t weight_before[kMaxGroups];
+    uint32_t tile_weight[kMaxGroups];
     Group groups[kMaxGroups];
 };
 

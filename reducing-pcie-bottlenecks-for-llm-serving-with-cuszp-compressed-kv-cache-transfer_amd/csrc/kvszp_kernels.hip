@@ -2146,6 +2146,26 @@ __device__ __forceinline__ uint32_t header_prefix(const uint8_t* in, uint32_t ti
     return total;
 }
 
+// First tile of workgroup b's run out of G: the tile where the cumulative
+// weight reaches b/G of the total (rounded up), so that every workgroup
+// moves about the same number of bytes.  Nondecreasing in b, 0 at b = 0
+// and total_tiles at b = G, so the runs tile [0, total_tiles) exactly.
+__device__ __forceinline__ uint32_t run_start(const DecompressParams& p, uint32_t b,
+                                              uint32_t G) {
+    if (p.total_weight == 0) return (uint32_t)((uint64_t)b * p.total_tiles / G);
+    if (b >= G) return p.total_tiles;
+    const uint64_t target = (uint64_t)b * p.total_weight / G;
+    int g = 0;
+    for (int k = 1; k < p.num_groups; ++k)
+        if (p.weight_before[k] <= target) g = k;
+    const uint32_t first = p.groups[g].first_tile;
+    const uint32_t tiles =
+        (g + 1 < p.num_groups ? p.groups[g + 1].first_tile : p.total_tiles) - first;
+    const uint64_t w = p.tile_weight[g];
+    const uint64_t i = (target - p.weight_before[g] + w - 1) / w;
+    return first + (uint32_t)(i < tiles ? i : tiles);
+}
+
 template <int kDst>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_persistent_kernel(
@@ -2160,8 +2180,8 @@ __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_
     if ((int)threadIdx.x < p.num_groups) s_gfirst[threadIdx.x] = p.groups[threadIdx.x].first_tile;
     __syncthreads();
     const uint32_t G = gridDim.x;
-    const uint32_t t_begin = (uint32_t)((uint64_t)blockIdx.x * p.total_tiles / G);
-    const uint32_t t_end = (uint32_t)((uint64_t)(blockIdx.x + 1) * p.total_tiles / G);
+    const uint32_t t_begin = run_start(p, blockIdx.x, G);
+    const uint32_t t_end = run_start(p, blockIdx.x + 1, G);
     if (t_begin >= t_end) return;  // whole workgroup
     uint32_t err = 0;
 
