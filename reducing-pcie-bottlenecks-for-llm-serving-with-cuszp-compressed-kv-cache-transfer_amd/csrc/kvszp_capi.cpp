@@ -577,7 +577,9 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
             uint64_t payload = 0;
             for (uint32_t k = 0; k < spec.jobs; ++k, ++j) payload += sizes[j] - g.header_bytes;
             const uint64_t tiles = (uint64_t)g.tiles_per_job * spec.jobs;
-            const uint64_t w = (2 * spec.n * spec.jobs + payload + tiles / 2) / tiles;
+            // Callers reject empty groups; the guard keeps the division defined.
+            const uint64_t w =
+                tiles ? (2 * spec.n * spec.jobs + payload + tiles / 2) / tiles : 1;
             p.tile_weight[gi] = (uint32_t)std::max<uint64_t>(w, 1);
             p.weight_before[gi] = before;
             before += tiles * p.tile_weight[gi];
