@@ -306,6 +306,44 @@ def test_grouped_indexed_scatter_matches_oracle(cpp, oracle, prefix, src, epl,
     assert np.array_equal(u16(ref), got)
 
 
+def test_grouped_indexed_scatter_skewed_groups(cpp, oracle):
+    """Groups of very different payloads in one launch: all-zero pages
+    (every block rate 0) beside random pages at REL 1e-6 (rates near 20,
+    high plane words).  The decoder's runs are balanced by bytes, so its
+    workgroups hold uneven tile counts, some none; every value must still
+    come out as the oracle decodes it."""
+    prefix, src, epl = 2, 6, 4096
+    groups = [[0, 1, 2], [3, 4, 5]]
+    counts = [3, 4]
+    n = prefix * 3 * epl
+    pages = [torch.zeros(counts[0], prefix * src * epl, dtype=torch.bfloat16, device=DEV),
+             rand_pages(counts[1], prefix * src * epl, seed=11)]
+    w = make(cpp)
+    bufs, sizes, bounds, idx_t, jobs = [], [], [], [], []
+    for g, layers in enumerate(groups):
+        it = torch.tensor(layers, dtype=torch.long, device=DEV)
+        b = buffers(cpp, counts[g], n)
+        ok, s, e = w.compress_batch_fixed_bf16_indexed(
+            list(pages[g]), b, it, prefix, src, epl, [1e-4 if g == 0 else 1e-6] * counts[g])
+        assert ok
+        bufs += b
+        sizes += list(s)
+        bounds += list(e)
+        idx_t.append(it)
+        jobs += [layers] * counts[g]
+    assert max(sizes[counts[0]:]) > 4 * min(sizes[:counts[0]])
+    dest = torch.full((len(jobs), prefix * src * epl), -2.0, dtype=torch.bfloat16, device=DEV)
+    assert w.decompress_batch_fixed_bf16_indexed_scatter_groups(
+        bufs, sizes, list(dest), idx_t, counts, prefix, src, epl, bounds)
+    assert w.synchronize()
+    got = u16(dest)
+    for k, layers in enumerate(jobs):
+        want = u16(torch.full((prefix * src * epl,), -2.0, dtype=torch.bfloat16))
+        oracle.decompress_indexed(bufs[k][:sizes[k]].cpu().numpy(), n, bounds[k], want,
+                                  layers, src, epl)
+        assert np.array_equal(got[k], want), f"job {k}"
+
+
 def test_grouped_indexed_scatter_rejects_bad_groups(cpp):
     full = rand_pages(2, 2 * 4 * 64, seed=3)
     w = make(cpp)
