@@ -114,8 +114,8 @@ int kvszp_compress_batch_fixed_bf16_indexed(
  * cuszp_wrapper.cpp:683-868 (pybind11_bindings.cpp:133-163).  Requests are
  * laid out group by group: group g covers the next group_sizes[g] entries of
  * inputs/outputs and uses layer_indices[g] (device int64, selected_layers[g]
- * long).  All groups run in ONE kernel launch (the reference launches once
- * per group). */
+ * long).  Up to 16 groups run in ONE kernel launch (the reference launches
+ * once per group); more groups take one launch per 16. */
 int kvszp_compress_batch_fixed_bf16_indexed_groups(
     kvszp_ctx* ctx, const void* const* inputs, void* const* outputs,
     const uint64_t* capacities, const int64_t* const* layer_indices,
@@ -171,6 +171,56 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups(
     const int64_t* const* layer_indices, const size_t* selected_layers,
     const size_t* group_sizes, size_t num_groups, size_t prefix_count,
     size_t source_layers, size_t elements_per_layer, kvszp_stream_t stream);
+
+/* ---- single-page fp32 API (fixed mode) ----------------------------------
+ * The reference serves these with upstream cuSZp's fp32 fixed-mode kernels
+ * (cuszp_fastpath.cu:5-64); the stream layout is the batched BF16 one
+ * (cuszp_batched_fixed.cu:52-54), so here the same kernels run with fp32
+ * loads and stores.  The relative bound is the one these methods compute:
+ * at::aminmax over the whole input (a NaN makes the bound NaN), range raised
+ * to 1e-6f when below it, eb = eps * range (cuszp_wrapper.cpp:249-257,
+ * :371-377).  Require MODE_FIXED, DIM_1D, TYPE_FLOAT; the plain/outlier modes
+ * of upstream cuSZp are not provided (KVSZP_EINVAL).  Inputs and outputs are
+ * contiguous fp32 arrays, 4-byte aligned. */
+
+/* Replaces CuSZpWrapper::compress (fixed mode), cuszp_wrapper.cpp:216-325
+ * (pybind11_bindings.cpp:49-64).  eps_override > 0 overrides error_bound.
+ * Blocks until *size_out (stream bytes S) and *bound_out are on the host. */
+int kvszp_compress_fixed_f32(kvszp_ctx* ctx, const float* input,
+                             size_t num_elements, void* output,
+                             uint64_t capacity, float eps_override,
+                             kvszp_stream_t stream, uint64_t* size_out,
+                             float* bound_out);
+
+/* Replaces CuSZpWrapper::compress_batch_fixed, cuszp_wrapper.cpp:327-429
+ * (pybind11_bindings.cpp:65-82): batch pages of num_elements fp32 values in
+ * one launch (the reference launches once per page). */
+int kvszp_compress_batch_fixed_f32(kvszp_ctx* ctx, const void* const* inputs,
+                                   void* const* outputs,
+                                   const uint64_t* capacities,
+                                   const float* eps_overrides, size_t batch,
+                                   size_t num_elements, kvszp_stream_t stream,
+                                   uint64_t* sizes_out, float* bounds_out);
+
+/* Replaces CuSZpWrapper::decompress (fixed mode), cuszp_wrapper.cpp:870-943
+ * (pybind11_bindings.cpp:164-173): num_elements fp32 values
+ * y = fl(fl(q * eb) * 2) to output; enqueue only. */
+int kvszp_decompress_fixed_f32(kvszp_ctx* ctx, const void* compressed,
+                               uint64_t compressed_size, float* output,
+                               size_t num_elements, float error_bound,
+                               kvszp_stream_t stream);
+
+/* Replaces CuSZpWrapper::decompress_batch (fixed mode),
+ * cuszp_wrapper.cpp:944-1033 (pybind11_bindings.cpp:174-189): page i
+ * (num_elements[i] values) to outputs[i], all pages in one launch per run of
+ * equal lengths (the reference fans pages out over up to 8 streams). */
+int kvszp_decompress_batch_fixed_f32(kvszp_ctx* ctx,
+                                     const void* const* compressed,
+                                     const uint64_t* sizes,
+                                     const float* error_bounds, size_t batch,
+                                     void* const* outputs,
+                                     const uint64_t* num_elements,
+                                     kvszp_stream_t stream);
 
 /* Waits for `stream` and reports any error a kernel of this context flagged
  * since the last check (decompress calls only enqueue, so their device-side

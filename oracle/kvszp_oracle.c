@@ -129,12 +129,24 @@ static void put_word(uint8_t* out, uint64_t pos, uint32_t word) {
     out[pos + 3] = (uint8_t)(word);
 }
 
+/* Where the encoder reads logical element i: a BF16 page (through the
+ * layer map) or a contiguous fp32 array. */
+typedef struct {
+    const uint16_t* page;
+    const float* f32;
+    const int64_t* layer_indices;
+    uint64_t sel, src, epl;
+} source_t;
+
+static float source_get(const source_t* s, uint64_t i) {
+    if (s->f32 != NULL) return s->f32[i];
+    return kvo_bf16_to_f32(
+        s->page[kvo_source_index(i, s->layer_indices, s->sel, s->src, s->epl)]);
+}
+
 /* compress_batch_fixed_bf16_kernel, cu:135-359, one page. */
-uint64_t kvo_compress_page(const uint16_t* page, uint64_t n,
-                           const int64_t* layer_indices,
-                           uint64_t selected_layers, uint64_t source_layers,
-                           uint64_t elements_per_layer, float eb, int variant,
-                           uint8_t* out) {
+static uint64_t encode_page(const source_t* in, uint64_t n, float eb,
+                            int variant, uint8_t* out) {
     const float recip = 0.5f / eb; /* cu:166 */
     const uint64_t nb = (n + KVO_BLOCK - 1) / KVO_BLOCK;
     const uint64_t header = kvo_header_bytes(n);
@@ -147,12 +159,8 @@ uint64_t kvo_compress_page(const uint16_t* page, uint64_t n,
         for (uint32_t v = 0; v < KVO_BLOCK; ++v) {
             const uint64_t i = b * KVO_BLOCK + v;
             int32_t q = 0;
-            if (i < n) { /* cu:200-211: tail elements quantize to 0 */
-                const uint64_t src = kvo_source_index(
-                    i, layer_indices, selected_layers, source_layers,
-                    elements_per_layer);
-                q = kvo_quantize(kvo_bf16_to_f32(page[src]), recip, variant);
-            }
+            if (i < n) /* cu:200-211: tail elements quantize to 0 */
+                q = kvo_quantize(source_get(in, i), recip, variant);
             uint32_t a = (uint32_t)q;
             if (q < 0) { /* cu:212-215 */
                 sign |= 1u << (31 - v);
@@ -177,9 +185,45 @@ uint64_t kvo_compress_page(const uint16_t* page, uint64_t n,
     return pos; /* = R + payload, cuszp_wrapper.cpp:534-541 */
 }
 
+uint64_t kvo_compress_page(const uint16_t* page, uint64_t n,
+                           const int64_t* layer_indices,
+                           uint64_t selected_layers, uint64_t source_layers,
+                           uint64_t elements_per_layer, float eb, int variant,
+                           uint8_t* out) {
+    const source_t s = {page, NULL, layer_indices, selected_layers,
+                        source_layers, elements_per_layer};
+    return encode_page(&s, n, eb, variant, out);
+}
+
+/* The fp32 single-page path (CuSZpWrapper::compress / compress_batch_fixed,
+ * cuszp_wrapper.cpp:216-429): the same stream over fp32 values.  The
+ * reference runs upstream cuSZp's fp32 fixed-mode kernel there, which is not
+ * vendored; cuszp_batched_fixed.cu:52-54 states that the batched BF16 layout
+ * is that kernel's.  Parity with upstream itself is unpinned. */
+uint64_t kvo_compress_page_f32(const float* x, uint64_t n, float eb,
+                               int variant, uint8_t* out) {
+    const source_t s = {NULL, x, NULL, 0, 0, 0};
+    return encode_page(&s, n, eb, variant, out);
+}
+
+/* at::aminmax over the whole input (NaN anywhere -> NaN extrema), range =
+ * max - min raised to 1e-6f when below it, eb = eps * range
+ * (cuszp_wrapper.cpp:249-257 and the std::max form at :371-377). */
+float kvo_relative_bound_f32(const float* x, uint64_t n, float eps) {
+    float lo = x[0], hi = x[0];
+    for (uint64_t i = 0; i < n; ++i) {
+        if (x[i] != x[i]) return eps * NAN;
+        if (x[i] < lo) lo = x[i];
+        if (x[i] > hi) hi = x[i];
+    }
+    float range = hi - lo;
+    if (range < 1e-6f) range = 1e-6f;
+    return eps * range;
+}
+
 /* Where the decoder puts logical element i. */
 typedef struct {
-    int kind; /* 0 contiguous, 1 scatter, 2 indexed */
+    int kind; /* 0 contiguous, 1 scatter, 2 indexed, 3 contiguous fp32 */
     uint16_t* out;
     uint16_t* const* destinations;
     uint64_t dpp, epd;
@@ -187,7 +231,12 @@ typedef struct {
     uint64_t sel, src, epl;
 } sink_t;
 
-static void sink_put(const sink_t* s, uint64_t i, uint16_t value) {
+static void sink_put(const sink_t* s, uint64_t i, float decoded) {
+    if (s->kind == 3) {
+        ((float*)(void*)s->out)[i] = decoded;
+        return;
+    }
+    const uint16_t value = kvo_f32_to_bf16_rne(decoded);
     switch (s->kind) {
     case 0: /* decoded + output_index (cu:569-576, 608-620) */
         s->out[i] = value;
@@ -215,7 +264,7 @@ static int decode_page(const uint8_t* in, uint64_t stream_size, uint64_t n,
         if (rate == 0) {
             if (rate0_policy == KVO_RATE0_ZERO)
                 for (uint32_t v = 0; v < KVO_BLOCK && b * KVO_BLOCK + v < n; ++v)
-                    sink_put(sink, b * KVO_BLOCK + v, 0);
+                    sink_put(sink, b * KVO_BLOCK + v, 0.0f);
             continue; /* cu:496: nothing written */
         }
         if (pos + 4u + 4u * (uint64_t)rate > stream_size) return -1;
@@ -238,7 +287,7 @@ static int decode_page(const uint8_t* in, uint64_t stream_size, uint64_t n,
             if (sign & (1u << (31 - v))) q = (int32_t)(0u - mag[v]); /* :528 */
             const float scaled = (float)q * eb;                       /* :535 */
             const float value = scaled * 2.0f;
-            sink_put(sink, i, kvo_f32_to_bf16_rne(value));
+            sink_put(sink, i, value); /* BF16 sinks round here (cu:538) */
         }
     }
     return 0;
@@ -268,6 +317,16 @@ int kvo_decompress_indexed(const uint8_t* stream, uint64_t stream_size,
                            uint64_t elements_per_layer) {
     sink_t s = {2, destination, NULL, 0, 0, layer_indices, selected_layers,
                 source_layers, elements_per_layer};
+    return decode_page(stream, stream_size, n, eb, rate0_policy, &s);
+}
+
+/* The fp32 single-page decode (CuSZpWrapper::decompress, fixed mode,
+ * cuszp_wrapper.cpp:870-943): y = fl(fl(q * eb) * 2) without the BF16
+ * rounding.  Upstream's fp32 decoder is not vendored (parity unpinned);
+ * kvo_f32_to_bf16_rne of this output is the BF16 decoders' value. */
+int kvo_decompress_f32(const uint8_t* stream, uint64_t stream_size, uint64_t n,
+                       float eb, int rate0_policy, float* out) {
+    sink_t s = {3, (uint16_t*)(void*)out, NULL, 0, 0, NULL, 0, 0, 0};
     return decode_page(stream, stream_size, n, eb, rate0_policy, &s);
 }
 

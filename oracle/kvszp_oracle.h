@@ -7,7 +7,8 @@
  * this library, and only as the checker (or the timed CPU baseline).  The
  * product path never calls it.
  *
- * BF16 values travel as raw uint16_t bit patterns.
+ * BF16 values travel as raw uint16_t bit patterns; the fp32 single-page path
+ * takes and returns float arrays.
  */
 #ifndef KVSZP_ORACLE_H
 #define KVSZP_ORACLE_H
@@ -52,6 +53,14 @@ uint64_t kvo_compress_page(const uint16_t* page, uint64_t n,
                            uint64_t selected_layers, uint64_t source_layers,
                            uint64_t elements_per_layer, float eb, int variant,
                            uint8_t* out);
+
+/* fp32 single-page path (CuSZpWrapper::compress/decompress, fixed mode):
+ * the same stream over contiguous fp32 values; bound as at::aminmax. */
+float kvo_relative_bound_f32(const float* x, uint64_t n, float eps);
+uint64_t kvo_compress_page_f32(const float* x, uint64_t n, float eb,
+                               int variant, uint8_t* out);
+int kvo_decompress_f32(const uint8_t* stream, uint64_t stream_size, uint64_t n,
+                       float eb, int rate0_policy, float* out);
 
 /* Decoders.  Each returns 0 on success, -1 if the stream is malformed
  * (rate > 31 or payload past stream_size). */

@@ -92,6 +92,15 @@ def lib() -> ctypes.CDLL:
         L.kvo_decompress_batch_contiguous.argtypes = [
             ctypes.c_void_p, ctypes.c_void_p, _u64, _u64, ctypes.c_void_p,
             ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        L.kvo_relative_bound_f32.restype = ctypes.c_float
+        L.kvo_relative_bound_f32.argtypes = [ctypes.c_void_p, _u64, ctypes.c_float]
+        L.kvo_compress_page_f32.restype = _u64
+        L.kvo_compress_page_f32.argtypes = [
+            ctypes.c_void_p, _u64, ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
+        L.kvo_decompress_f32.restype = ctypes.c_int
+        L.kvo_decompress_f32.argtypes = [
+            ctypes.c_void_p, _u64, _u64, ctypes.c_float, ctypes.c_int,
+            ctypes.c_void_p]
         L.kvo_int8_encode.restype = ctypes.c_float
         L.kvo_int8_encode.argtypes = [ctypes.c_void_p, _u64, ctypes.c_void_p]
         L.kvo_int8_decode.restype = None
@@ -167,7 +176,9 @@ def relative_bound(page, n: int, eps: float, layer_indices=None,
 
 
 def max_stream_bytes(n: int) -> int:
-    return header_bytes(n) + 4 * n + 4 * ((n + BLOCK - 1) // BLOCK)
+    """Largest stream of n values: the header plus 4 + 4*31 bytes for every
+    block, partial ones included (a block of one value can have rate 31)."""
+    return header_bytes(n) + 128 * ((n + BLOCK - 1) // BLOCK)
 
 
 def compress_page(page, n: int, eb: float, layer_indices=None,
@@ -259,6 +270,45 @@ def compress_batch(pages: np.ndarray, eps, default_eps: float = 1e-4,
     if return_elapsed:
         return streams, sizes, bounds, elapsed
     return streams, sizes, bounds
+
+
+# ---- fp32 single-page path (CuSZpWrapper::compress / decompress) -----------
+
+def _as_f32(a) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    if a.dtype != np.float32:
+        raise TypeError("fp32 pages must be float32 arrays")
+    return a
+
+
+def relative_bound_f32(x, eps: float) -> float:
+    """at::aminmax bound of cuszp_wrapper.cpp:249-257 (NaN propagates)."""
+    x = _as_f32(x)
+    return float(lib().kvo_relative_bound_f32(x.ctypes.data, x.size, eps))
+
+
+def compress_page_f32(x, eb: float,
+                      variant: int = QUANT_TWO_ROUNDINGS) -> np.ndarray:
+    """Encode a contiguous fp32 page; returns the S stream bytes."""
+    x = _as_f32(x)
+    out = np.zeros(max_stream_bytes(x.size), dtype=np.uint8)
+    size = lib().kvo_compress_page_f32(x.ctypes.data, x.size, eb, variant,
+                                       out.ctypes.data)
+    return out[:size].copy()
+
+
+def decompress_f32(stream, n: int, eb: float,
+                   rate0_policy: int = RATE0_ZERO,
+                   out: np.ndarray | None = None) -> np.ndarray:
+    """fp32 decode y = fl(fl(q*eb)*2) of n values."""
+    stream = np.ascontiguousarray(np.asarray(stream, dtype=np.uint8))
+    if out is None:
+        out = np.zeros(n, dtype=np.float32)
+    rc = lib().kvo_decompress_f32(stream.ctypes.data, stream.size, n, eb,
+                                  rate0_policy, out.ctypes.data)
+    if rc != 0:
+        raise ValueError("malformed fixed-mode stream")
+    return out
 
 
 def int8_encode(page) -> tuple[np.ndarray, float]:

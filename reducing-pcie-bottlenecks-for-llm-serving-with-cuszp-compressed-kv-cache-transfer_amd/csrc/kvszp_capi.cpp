@@ -328,62 +328,100 @@ int validate_layers(const int64_t* layers, uint64_t sel, uint64_t prefix,
     return KVSZP_OK;
 }
 
-// Common compress path: `specs` are the groups, requests laid out group by
-// group in inputs/outputs.
-int compress_groups(kvszp_ctx* c, const void* const* inputs,
-                    void* const* outputs, const uint64_t* capacities,
-                    const float* eps_overrides, size_t batch,
-                    const std::vector<GroupSpec>& specs, hipStream_t stream,
-                    uint64_t* sizes_out, float* bounds_out) {
-    int rc = check_fixed_config(c);
-    if (rc) return rc;
-    if (batch == 0) return fail(KVSZP_EINVAL, "empty batch");
-    if (!inputs || !outputs || !sizes_out || !bounds_out)
-        return fail(KVSZP_EINVAL, "null pointer argument");
-    if (specs.empty() || specs.size() > (size_t)kMaxGroups)
-        return fail(KVSZP_EINVAL, "between 1 and %d groups supported", kMaxGroups);
-    rc = use_device(c);
-    if (rc) return rc;
+// One launch's share of a call: groups [g0, g1) of the call's specs, with
+// job numbers global to the call and tile numbers local to the launch.
+struct Chunk {
+    size_t g0, g1;
+    uint64_t tiles;
+    uint32_t max_tiles_per_job;
+    bool whole_blocks;  // every block whole and inside one layer
+};
 
-    CompressParams p;
-    std::memset(&p, 0, sizeof(p));
-    std::vector<CompressJob> jobs(batch);
-    bool aligned16 = true;
-    bool whole_blocks = true;  // every block whole and inside one layer
-    uint64_t total_tiles = 0;
-    uint32_t max_tiles_per_job = 0;
-    size_t job = 0;
-    for (size_t gi = 0; gi < specs.size(); ++gi) {
+// Splits `specs` into launches of at most kMaxGroups groups (the group
+// records travel as kernel arguments).  The reference takes any number of
+// groups (cuszp_wrapper.cpp:683-868, one launch per group).
+std::vector<Chunk> split_chunks(const std::vector<GroupSpec>& specs) {
+    std::vector<Chunk> chunks;
+    for (size_t g0 = 0; g0 < specs.size(); g0 += kMaxGroups) {
+        Chunk ch{g0, std::min(specs.size(), g0 + (size_t)kMaxGroups), 0, 0, true};
+        for (size_t gi = ch.g0; gi < ch.g1; ++gi) {
+            const GroupSpec& s = specs[gi];
+            const uint32_t tpj = (uint32_t)((s.n + kTileElems - 1) / kTileElems);
+            ch.tiles += (uint64_t)tpj * s.jobs;
+            ch.max_tiles_per_job = std::max(ch.max_tiles_per_job, tpj);
+            if ((s.n % kBlockElems) != 0 || (s.layers && (s.epl % kBlockElems) != 0))
+                ch.whole_blocks = false;
+        }
+        chunks.push_back(ch);
+    }
+    return chunks;
+}
+
+// Group records of one chunk; `first_job` is the call-wide job number of
+// the chunk's first request.
+int fill_groups(Group* groups, const std::vector<GroupSpec>& specs, const Chunk& ch,
+                size_t first_job) {
+    uint64_t tiles = 0;
+    size_t job = first_job;
+    for (size_t gi = ch.g0; gi < ch.g1; ++gi) {
         const GroupSpec& s = specs[gi];
-        if (s.n == 0 || s.n > kMaxElements)
-            return fail(KVSZP_EINVAL, "segment of %llu elements unsupported",
-                        (unsigned long long)s.n);
-        Group& g = p.groups[gi];
+        Group& g = groups[gi - ch.g0];
         g.n = s.n;
         g.layers = s.layers;
         g.selected_layers = s.sel;
         g.source_layers = s.src;
         g.elements_per_layer = s.epl;
         g.first_job = (uint32_t)job;
-        g.first_tile = (uint32_t)total_tiles;
+        g.first_tile = (uint32_t)tiles;
         g.tiles_per_job = (uint32_t)((s.n + kTileElems - 1) / kTileElems);
         g.header_bytes = header_bytes_of(s.n);
-        max_tiles_per_job = std::max(max_tiles_per_job, g.tiles_per_job);
-        total_tiles += (uint64_t)g.tiles_per_job * s.jobs;
+        tiles += (uint64_t)g.tiles_per_job * s.jobs;
+        job += s.jobs;
+    }
+    return (int)(ch.g1 - ch.g0);
+}
+
+// Common compress path: `specs` are the groups, requests laid out group by
+// group in inputs/outputs.  `f32`: contiguous fp32 pages (the single-page
+// API, cuszp_wrapper.cpp:216-429) instead of BF16 pages.
+int compress_groups(kvszp_ctx* c, const void* const* inputs,
+                    void* const* outputs, const uint64_t* capacities,
+                    const float* eps_overrides, size_t batch,
+                    const std::vector<GroupSpec>& specs, hipStream_t stream,
+                    uint64_t* sizes_out, float* bounds_out, bool f32 = false) {
+    int rc = check_fixed_config(c);
+    if (rc) return rc;
+    if (batch == 0) return fail(KVSZP_EINVAL, "empty batch");
+    if (!inputs || !outputs || !sizes_out || !bounds_out)
+        return fail(KVSZP_EINVAL, "null pointer argument");
+    if (specs.empty()) return fail(KVSZP_EINVAL, "no groups");
+    rc = use_device(c);
+    if (rc) return rc;
+
+    const uintptr_t elem_align = f32 ? 3u : 1u;
+    std::vector<CompressJob> jobs(batch);
+    bool aligned16 = true;
+    size_t job = 0;
+    for (size_t gi = 0; gi < specs.size(); ++gi) {
+        const GroupSpec& s = specs[gi];
+        if (s.n == 0 || s.n > kMaxElements)
+            return fail(KVSZP_EINVAL, "segment of %llu elements unsupported",
+                        (unsigned long long)s.n);
+        if (f32 && s.layers) return fail(KVSZP_EINVAL, "fp32 pages take no layer map");
         if (s.layers && (s.epl % 8) != 0) aligned16 = false;
-        if ((s.n % kBlockElems) != 0 || (s.layers && (s.epl % kBlockElems) != 0))
-            whole_blocks = false;
         // cuszp_wrapper.cpp:449-450 asks for capacity >= estimate(4n) = 8n.
         // That does not cover the header of tiny segments (R = 1024 bytes for
         // n < 128), so the worst-case stream R + 128 * nb is required too.
-        const uint64_t worst = g.header_bytes + 128ull * ((s.n + 31) / 32);
+        const uint64_t worst = header_bytes_of(s.n) + 128ull * ((s.n + 31) / 32);
         const uint64_t need = std::max<uint64_t>(8ull * s.n, worst);
         for (uint32_t k = 0; k < s.jobs; ++k, ++job) {
             if (job >= batch) return fail(KVSZP_EINVAL, "group sizes exceed batch");
             const uintptr_t in = (uintptr_t)inputs[job];
             const uintptr_t out = (uintptr_t)outputs[job];
             if (!in || !out) return fail(KVSZP_EINVAL, "null page pointer %zu", job);
-            if (in & 1u) return fail(KVSZP_EINVAL, "input %zu not 2-byte aligned", job);
+            if (in & elem_align)
+                return fail(KVSZP_EINVAL, "input %zu not %u-byte aligned", job,
+                            (unsigned)elem_align + 1u);
             if (out & 3u)
                 return fail(KVSZP_EINVAL, "compressed buffer %zu not 4-byte aligned", job);
             if (capacities && capacities[job] < need)
@@ -402,98 +440,121 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         }
     }
     if (job != batch) return fail(KVSZP_EINVAL, "group sizes do not cover the batch");
-    if (total_tiles == 0 || total_tiles > kMaxTiles)
-        return fail(KVSZP_EINVAL, "batch too large for one launch");
+    const std::vector<Chunk> chunks = split_chunks(specs);
+    uint64_t max_tiles = 0;
+    for (const Chunk& ch : chunks) {
+        if (ch.tiles == 0 || ch.tiles > kMaxTiles)
+            return fail(KVSZP_EINVAL, "batch too large for one launch");
+        max_tiles = std::max(max_tiles, ch.tiles);
+    }
 
     const bool relative = c->config.use_relative_error != 0;
-    int bound_mode = kBoundAbsolute;
-    if (relative)
-        bound_mode = (max_tiles_per_job <= c->fused_tile_limit) ? kBoundFused
-                                                                : kBoundPrepass;
-
     // Workspaces.
-    if ((rc = ensure(c->tile_state, total_tiles * 8, true, stream)) ||
-        (rc = ensure(c->tile_minmax, total_tiles * 8, true, stream)) ||
+    if ((rc = ensure(c->tile_state, max_tiles * 8, true, stream)) ||
+        (rc = ensure(c->tile_minmax, max_tiles * 8, true, stream)) ||
         (rc = ensure(c->job_minmax, batch * 16, true, stream)) ||
         (rc = ensure_host_results(c, batch * 8)))
         return rc;
     const uint32_t seq = ++c->seq;
     rc = upload_tables(c, jobs.data(), batch * sizeof(CompressJob), seq, stream);
     if (rc) return rc;
-    uint32_t epoch;
-    if ((rc = next_epoch(c, stream, &epoch))) return rc;
 
     uint32_t* host_sizes = reinterpret_cast<uint32_t*>(c->host_results);
     float* host_bounds = reinterpret_cast<float*>(host_sizes + batch);
     const CompressJob* djobs = reinterpret_cast<const CompressJob*>(c->tables.ptr);
 
-    hipError_t e;
-    const int rec = timing_begin(c, KVSZP_KERNEL_COMPRESS);
-    if (bound_mode == kBoundPrepass) {
-        MinMaxParams m;
-        std::memset(&m, 0, sizeof(m));
-        m.jobs = djobs;
-        m.job_minmax = reinterpret_cast<unsigned long long*>(c->job_minmax.ptr);
-        m.error = error_word(c);
-        m.host_ctl = c->host_ctl;
-        m.seq = seq;
-        m.epoch = epoch;
-        m.num_groups = (int)specs.size();
-        std::memcpy(m.groups, p.groups, sizeof(m.groups));
-        e = launch_minmax(m, (uint32_t)total_tiles, stream, timing_start(c, rec));
-        if (e != hipSuccess) return hip_fail(e, "minmax launch");
+    // One launch per chunk (normally one); all share the call's sequence
+    // number and table, each has its own epoch (the look-back and min/max
+    // words are reused from launch to launch).
+    std::vector<CompressParams> launched(chunks.size());
+    std::vector<char> persistent(chunks.size(), 0);
+    size_t first_job = 0;
+    for (size_t k = 0; k < chunks.size(); ++k) {
+        const Chunk& ch = chunks[k];
+        CompressParams& p = launched[k];
+        std::memset(&p, 0, sizeof(p));
+        p.num_groups = fill_groups(p.groups, specs, ch, first_job);
+        for (size_t gi = ch.g0; gi < ch.g1; ++gi) first_job += specs[gi].jobs;
+        int bound_mode = kBoundAbsolute;
+        if (relative)
+            bound_mode = (!f32 && ch.max_tiles_per_job <= c->fused_tile_limit)
+                             ? kBoundFused : kBoundPrepass;
+        uint32_t epoch;
+        if ((rc = next_epoch(c, stream, &epoch))) return rc;
+        const int rec = timing_begin(c, KVSZP_KERNEL_COMPRESS);
+        hipError_t e;
+        if (bound_mode == kBoundPrepass) {
+            MinMaxParams m;
+            std::memset(&m, 0, sizeof(m));
+            m.jobs = djobs;
+            m.job_minmax = reinterpret_cast<unsigned long long*>(c->job_minmax.ptr);
+            m.error = error_word(c);
+            m.host_ctl = c->host_ctl;
+            m.seq = seq;
+            m.epoch = epoch;
+            m.num_groups = p.num_groups;
+            m.input_f32 = f32 ? 1 : 0;
+            std::memcpy(m.groups, p.groups, sizeof(m.groups));
+            e = launch_minmax(m, (uint32_t)ch.tiles, stream, timing_start(c, rec));
+            if (e != hipSuccess) return hip_fail(e, "minmax launch");
+        }
+        p.jobs = djobs;
+        p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
+        p.tile_minmax = reinterpret_cast<unsigned long long*>(c->tile_minmax.ptr);
+        p.job_minmax = reinterpret_cast<const unsigned long long*>(c->job_minmax.ptr);
+        p.host_sizes = host_sizes;
+        p.host_bounds = host_bounds;
+        p.error = error_word(c);
+        p.host_ctl = c->host_ctl;
+        p.seq = seq;
+        p.ticket = c->use_tickets ? c->control : nullptr;
+        p.ticket_base = c->ticket_next;
+        p.epoch = epoch;
+        p.total_tiles = (uint32_t)ch.tiles;
+        p.bound_mode = bound_mode;
+        p.quantizer = c->quantizer;
+        p.aligned16 = aligned16 ? 1 : 0;
+        p.input_f32 = f32 ? 1 : 0;
+        persistent[k] = !f32 && bound_mode != kBoundPrepass && c->pipelined_grid != 0 &&
+                        ch.whole_blocks && aligned16 &&
+                        ch.max_tiles_per_job <= c->pipelined_grid / 2;
+        if (persistent[k]) {
+            // Persistent encoder (whole, aligned, single-layer blocks only); its
+            // waits are cycle-free while a job's tiles number at most the grid
+            // (half of it here, for margin).
+            CompressParams pp = p;
+            pp.ticket = nullptr;
+            const uint32_t grid = (uint32_t)std::min<uint64_t>(ch.tiles, c->pipelined_grid);
+            e = launch_compress_pipelined(pp, grid, stream, timing_start(c, rec),
+                                          timing_stop(c, rec));
+        } else {
+            e = launch_compress(p, stream,
+                                bound_mode == kBoundPrepass ? nullptr : timing_start(c, rec),
+                                timing_stop(c, rec));
+        }
+        if (e != hipSuccess) return hip_fail(e, "compress launch");
+        c->ticket_next += ch.tiles;
     }
-    p.jobs = djobs;
-    p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
-    p.tile_minmax = reinterpret_cast<unsigned long long*>(c->tile_minmax.ptr);
-    p.job_minmax = reinterpret_cast<const unsigned long long*>(c->job_minmax.ptr);
-    p.host_sizes = host_sizes;
-    p.host_bounds = host_bounds;
-    p.error = error_word(c);
-    p.host_ctl = c->host_ctl;
-    p.seq = seq;
-    p.ticket = c->use_tickets ? c->control : nullptr;
-    p.ticket_base = c->ticket_next;
-    p.epoch = epoch;
-    p.total_tiles = (uint32_t)total_tiles;
-    p.num_groups = (int)specs.size();
-    p.bound_mode = bound_mode;
-    p.quantizer = c->quantizer;
-    p.aligned16 = aligned16 ? 1 : 0;
-    const bool persistent = bound_mode != kBoundPrepass && c->pipelined_grid != 0 &&
-                            whole_blocks && aligned16 &&
-                            max_tiles_per_job <= c->pipelined_grid / 2;
-    if (persistent) {
-        // Persistent encoder (whole, aligned, single-layer blocks only); its
-        // waits are cycle-free while a job's tiles number at most the grid
-        // (half of it here, for margin).
-        CompressParams pp = p;
-        pp.ticket = nullptr;
-        const uint32_t grid = (uint32_t)std::min<uint64_t>(total_tiles, c->pipelined_grid);
-        e = launch_compress_pipelined(pp, grid, stream, timing_start(c, rec),
-                                      timing_stop(c, rec));
-    } else {
-        e = launch_compress(p, stream,
-                            bound_mode == kBoundPrepass ? nullptr : timing_start(c, rec),
-                            timing_stop(c, rec));
-    }
-    if (e != hipSuccess) return hip_fail(e, "compress launch");
-    c->ticket_next += total_tiles;
 
     // The encoder wrote sizes and bounds into pinned host memory; wait for it,
     // since callers need the sizes on the host (cuszp_wrapper.cpp:520-532).
-    e = wait_stream(stream);
+    hipError_t e = wait_stream(stream);
     if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
-    if (persistent && __atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq) {
+    if (__atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq) {
         // Some wave's payload was too large for the persistent encoder's
-        // staging words (rates near 31 throughout): encode the launch again
-        // with one workgroup per tile, under a fresh epoch.
-        if ((rc = next_epoch(c, stream, &epoch))) return rc;
-        p.epoch = epoch;
-        p.ticket_base = c->ticket_next;
-        e = launch_compress(p, stream, nullptr, timing_stop(c, rec));
-        if (e != hipSuccess) return hip_fail(e, "compress launch");
-        c->ticket_next += total_tiles;
+        // staging words (rates near 31 throughout): encode those launches
+        // again with one workgroup per tile, under fresh epochs.
+        for (size_t k = 0; k < chunks.size(); ++k) {
+            if (!persistent[k]) continue;
+            CompressParams p = launched[k];
+            uint32_t epoch;
+            if ((rc = next_epoch(c, stream, &epoch))) return rc;
+            p.epoch = epoch;
+            p.ticket_base = c->ticket_next;
+            e = launch_compress(p, stream, nullptr, nullptr);
+            if (e != hipSuccess) return hip_fail(e, "compress launch");
+            c->ticket_next += chunks[k].tiles;
+        }
         e = wait_stream(stream);
         if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
     }
@@ -507,21 +568,19 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
 }
 
 // Common decompress path: `specs` are the groups, requests laid out group by
-// group (one launch for all of them).
+// group (one launch per kMaxGroups groups).  `f32`: fp32 values into
+// contiguous per-job outputs (kDstLinear).
 int decompress_groups(kvszp_ctx* c, const void* const* compressed,
                       const uint64_t* sizes, const float* bounds, size_t batch,
                       const std::vector<GroupSpec>& specs, int dst_kind,
                       const std::vector<uint16_t*>& dst_base,
                       const std::vector<uint16_t*>& dest_table, uint64_t dpp,
-                      uint64_t epd, bool aligned16, hipStream_t stream) {
+                      uint64_t epd, bool aligned16, hipStream_t stream,
+                      bool f32 = false) {
     int rc = use_device(c);
     if (rc) return rc;
-    if (specs.empty() || specs.size() > (size_t)kMaxGroups)
-        return fail(KVSZP_EINVAL, "between 1 and %d groups supported", kMaxGroups);
-    DecompressParams p;
-    std::memset(&p, 0, sizeof(p));
+    if (specs.empty()) return fail(KVSZP_EINVAL, "no groups");
     std::vector<DecompressJob> jobs(batch);
-    uint64_t total_tiles = 0;
     size_t job = 0;
     for (size_t gi = 0; gi < specs.size(); ++gi) {
         const GroupSpec& spec = specs[gi];
@@ -529,17 +588,6 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
             return fail(KVSZP_EINVAL, "segment of %llu elements unsupported",
                         (unsigned long long)spec.n);
         const uint32_t R = header_bytes_of(spec.n);
-        Group& g = p.groups[gi];
-        g.n = spec.n;
-        g.layers = spec.layers;
-        g.selected_layers = spec.sel;
-        g.source_layers = spec.src;
-        g.elements_per_layer = spec.epl;
-        g.first_job = (uint32_t)job;
-        g.first_tile = (uint32_t)total_tiles;
-        g.tiles_per_job = (uint32_t)((spec.n + kTileElems - 1) / kTileElems);
-        g.header_bytes = R;
-        total_tiles += (uint64_t)g.tiles_per_job * spec.jobs;
         for (uint32_t k = 0; k < spec.jobs; ++k, ++job) {
             if (job >= batch) return fail(KVSZP_EINVAL, "group sizes exceed batch");
             const size_t i = job;
@@ -562,29 +610,11 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         }
     }
     if (job != batch) return fail(KVSZP_EINVAL, "group sizes do not cover the batch");
-    if (total_tiles > kMaxTiles) return fail(KVSZP_EINVAL, "batch too large for one launch");
-
-    // Persistent decoder: per-group tile weights (BF16 output plus the
-    // group's average payload per tile), so that workgroups holding tiles of
-    // a high-rate group get fewer of them.  Kernel arguments only: the table
-    // keeps its size.
-    {
-        uint64_t before = 0;
-        size_t j = 0;
-        for (size_t gi = 0; gi < specs.size(); ++gi) {
-            const GroupSpec& spec = specs[gi];
-            const Group& g = p.groups[gi];
-            uint64_t payload = 0;
-            for (uint32_t k = 0; k < spec.jobs; ++k, ++j) payload += sizes[j] - g.header_bytes;
-            const uint64_t tiles = (uint64_t)g.tiles_per_job * spec.jobs;
-            // Callers reject empty groups; the guard keeps the division defined.
-            const uint64_t w =
-                tiles ? (2 * spec.n * spec.jobs + payload + tiles / 2) / tiles : 1;
-            p.tile_weight[gi] = (uint32_t)std::max<uint64_t>(w, 1);
-            p.weight_before[gi] = before;
-            before += tiles * p.tile_weight[gi];
-        }
-        p.total_weight = before;
+    const std::vector<Chunk> chunks = split_chunks(specs);
+    uint64_t max_tiles = 0;
+    for (const Chunk& ch : chunks) {
+        if (ch.tiles > kMaxTiles) return fail(KVSZP_EINVAL, "batch too large for one launch");
+        max_tiles = std::max(max_tiles, ch.tiles);
     }
 
     // Packed table: jobs, then (kDstMulti) the destination pointers.
@@ -594,41 +624,71 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     if (!dest_table.empty())
         std::memcpy(table.data() + jobs_bytes, dest_table.data(),
                     dest_table.size() * sizeof(uint16_t*));
-    if ((rc = ensure(c->tile_state, total_tiles * 8, true, stream))) return rc;
+    if ((rc = ensure(c->tile_state, max_tiles * 8, true, stream))) return rc;
     const uint32_t seq = ++c->seq;
     if ((rc = upload_tables(c, table.data(), table.size(), seq, stream))) return rc;
-    uint32_t epoch;
-    if ((rc = next_epoch(c, stream, &epoch))) return rc;
 
-    p.jobs = reinterpret_cast<const DecompressJob*>(c->tables.ptr);
-    p.dests = reinterpret_cast<uint16_t* const*>(
-        reinterpret_cast<char*>(c->tables.ptr) + jobs_bytes);
-    p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
-    p.error = error_word(c);
-    p.host_ctl = c->host_ctl;
-    p.seq = seq;
-    p.ticket = c->use_tickets ? c->control : nullptr;
-    p.ticket_base = c->ticket_next;
-    p.epoch = epoch;
-    p.total_tiles = (uint32_t)total_tiles;
-    p.num_groups = (int)specs.size();
-    p.dst_kind = dst_kind;
-    p.rate0_zero = c->rate0 == KVSZP_RATE0_ZERO ? 1 : 0;
-    p.aligned16 = aligned16 ? 1 : 0;
-    p.dests_per_page = dpp;
-    p.elements_per_dest = epd;
-    const int rec = timing_begin(c, KVSZP_KERNEL_DECOMPRESS);
-    hipError_t e;
-    if (c->decompress_grid != 0) {
-        p.ticket = nullptr;
-        const uint32_t grid = (uint32_t)std::min<uint64_t>(total_tiles, c->decompress_grid);
-        e = launch_decompress_persistent(p, grid, stream, timing_start(c, rec),
-                                         timing_stop(c, rec));
-    } else {
-        e = launch_decompress(p, stream, timing_start(c, rec), timing_stop(c, rec));
+    size_t first_job = 0;
+    for (const Chunk& ch : chunks) {
+        DecompressParams p;
+        std::memset(&p, 0, sizeof(p));
+        p.num_groups = fill_groups(p.groups, specs, ch, first_job);
+        // Persistent decoder: per-group tile weights (BF16 output plus the
+        // group's average payload per tile), so that workgroups holding tiles
+        // of a high-rate group get fewer of them.  Kernel arguments only: the
+        // table keeps its size.
+        {
+            uint64_t before = 0;
+            size_t j = first_job;
+            for (size_t gi = ch.g0; gi < ch.g1; ++gi) {
+                const GroupSpec& spec = specs[gi];
+                const Group& g = p.groups[gi - ch.g0];
+                uint64_t payload = 0;
+                for (uint32_t k = 0; k < spec.jobs; ++k, ++j) payload += sizes[j] - g.header_bytes;
+                const uint64_t tiles = (uint64_t)g.tiles_per_job * spec.jobs;
+                // Callers reject empty groups; the guard keeps the division defined.
+                const uint64_t w =
+                    tiles ? (2 * spec.n * spec.jobs + payload + tiles / 2) / tiles : 1;
+                p.tile_weight[gi - ch.g0] = (uint32_t)std::max<uint64_t>(w, 1);
+                p.weight_before[gi - ch.g0] = before;
+                before += tiles * p.tile_weight[gi - ch.g0];
+            }
+            p.total_weight = before;
+        }
+        for (size_t gi = ch.g0; gi < ch.g1; ++gi) first_job += specs[gi].jobs;
+        if (ch.tiles == 0) continue;
+        uint32_t epoch;
+        if ((rc = next_epoch(c, stream, &epoch))) return rc;
+        p.jobs = reinterpret_cast<const DecompressJob*>(c->tables.ptr);
+        p.dests = reinterpret_cast<uint16_t* const*>(
+            reinterpret_cast<char*>(c->tables.ptr) + jobs_bytes);
+        p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
+        p.error = error_word(c);
+        p.host_ctl = c->host_ctl;
+        p.seq = seq;
+        p.ticket = c->use_tickets ? c->control : nullptr;
+        p.ticket_base = c->ticket_next;
+        p.epoch = epoch;
+        p.total_tiles = (uint32_t)ch.tiles;
+        p.dst_kind = dst_kind;
+        p.rate0_zero = c->rate0 == KVSZP_RATE0_ZERO ? 1 : 0;
+        p.aligned16 = aligned16 ? 1 : 0;
+        p.output_f32 = f32 ? 1 : 0;
+        p.dests_per_page = dpp;
+        p.elements_per_dest = epd;
+        const int rec = timing_begin(c, KVSZP_KERNEL_DECOMPRESS);
+        hipError_t e;
+        if (c->decompress_grid != 0 && !f32) {
+            p.ticket = nullptr;
+            const uint32_t grid = (uint32_t)std::min<uint64_t>(ch.tiles, c->decompress_grid);
+            e = launch_decompress_persistent(p, grid, stream, timing_start(c, rec),
+                                             timing_stop(c, rec));
+        } else {
+            e = launch_decompress(p, stream, timing_start(c, rec), timing_stop(c, rec));
+        }
+        if (e != hipSuccess) return hip_fail(e, "decompress launch");
+        c->ticket_next += ch.tiles;
     }
-    if (e != hipSuccess) return hip_fail(e, "decompress launch");
-    c->ticket_next += total_tiles;
     return KVSZP_OK;
 }
 
@@ -946,6 +1006,80 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups(
     return decompress_groups(c, compressed, sizes, error_bounds, batch, specs,
                              kDstIndexed, dests, {}, 0, 0, false,
                              (hipStream_t)stream);
+}
+
+int kvszp_compress_fixed_f32(kvszp_ctx* c, const float* input, size_t num_elements,
+                             void* output, uint64_t capacity, float eps_override,
+                             kvszp_stream_t stream, uint64_t* size_out,
+                             float* bound_out) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (num_elements == 0) return fail(KVSZP_EINVAL, "empty input");
+    const void* in = input;
+    void* out = output;
+    const float eps = eps_override;  // <= 0: config.error_bound (cpp:241)
+    std::vector<GroupSpec> specs{GroupSpec{num_elements, nullptr, 0, 0, 0, 1}};
+    return compress_groups(c, &in, &out, &capacity, &eps, 1, specs,
+                           (hipStream_t)stream, size_out, bound_out, true);
+}
+
+int kvszp_compress_batch_fixed_f32(kvszp_ctx* c, const void* const* inputs,
+                                   void* const* outputs, const uint64_t* capacities,
+                                   const float* eps_overrides, size_t batch,
+                                   size_t num_elements, kvszp_stream_t stream,
+                                   uint64_t* sizes_out, float* bounds_out) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    std::vector<GroupSpec> specs{
+        GroupSpec{num_elements, nullptr, 0, 0, 0, (uint32_t)batch}};
+    return compress_groups(c, inputs, outputs, capacities, eps_overrides, batch,
+                           specs, (hipStream_t)stream, sizes_out, bounds_out, true);
+}
+
+// Contiguous fp32 outputs, one per request, grouped by equal length.
+static int decompress_f32(kvszp_ctx* c, const void* const* compressed,
+                          const uint64_t* sizes, const float* error_bounds,
+                          size_t batch, void* const* outputs,
+                          const uint64_t* num_elements, hipStream_t stream) {
+    int rc = check_fixed_config(c);
+    if (rc) return rc;
+    if (!compressed || !sizes || !error_bounds || !outputs || !num_elements)
+        return fail(KVSZP_EINVAL, "null pointer argument");
+    std::vector<GroupSpec> specs;
+    std::vector<uint16_t*> base(batch);
+    bool aligned16 = true;
+    for (size_t i = 0; i < batch; ++i) {
+        const uintptr_t d = (uintptr_t)outputs[i];
+        if (!d || (d & 3u)) return fail(KVSZP_EINVAL, "invalid fp32 output %zu", i);
+        if (num_elements[i] == 0) return fail(KVSZP_EINVAL, "empty output %zu", i);
+        if (d & 15u) aligned16 = false;
+        base[i] = reinterpret_cast<uint16_t*>(d);
+        if (specs.empty() || specs.back().n != num_elements[i])
+            specs.push_back(GroupSpec{num_elements[i], nullptr, 0, 0, 0, 0});
+        specs.back().jobs += 1;
+    }
+    return decompress_groups(c, compressed, sizes, error_bounds, batch, specs,
+                             kDstLinear, base, {}, 0, 0, aligned16, stream, true);
+}
+
+int kvszp_decompress_fixed_f32(kvszp_ctx* c, const void* compressed,
+                               uint64_t compressed_size, float* output,
+                               size_t num_elements, float error_bound,
+                               kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    void* out = output;
+    const uint64_t n = num_elements;
+    return decompress_f32(c, &compressed, &compressed_size, &error_bound, 1, &out, &n,
+                          (hipStream_t)stream);
+}
+
+int kvszp_decompress_batch_fixed_f32(kvszp_ctx* c, const void* const* compressed,
+                                     const uint64_t* sizes, const float* error_bounds,
+                                     size_t batch, void* const* outputs,
+                                     const uint64_t* num_elements,
+                                     kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (batch == 0) return KVSZP_OK;  // cuszp_wrapper.cpp:950
+    return decompress_f32(c, compressed, sizes, error_bounds, batch, outputs,
+                          num_elements, (hipStream_t)stream);
 }
 
 int kvszp_synchronize(kvszp_ctx* c, kvszp_stream_t stream) {

@@ -7,9 +7,8 @@
 // fixed-rate blocks (kTileBlocks * 32 elements); one workgroup of
 // kTileBlocks threads handles one tile, one thread per 32-element block.
 // Tiles are numbered group by group, job by job, so the tiles of a job are
-// consecutive.  Workgroups take tile numbers from a ticket counter, so a
-// tile only ever waits for tiles that already started (forward progress
-// does not depend on dispatch order).
+// consecutive.  A launch holds at most kMaxGroups groups (the records are
+// kernel arguments); the host splits larger calls into several launches.
 #ifndef KVSZP_INTERNAL_H
 #define KVSZP_INTERNAL_H
 
@@ -103,6 +102,7 @@ struct CompressParams {
     int bound_mode;
     int quantizer;                    // 0 two roundings, 1 fused
     int aligned16;                    // every input page is 16-byte aligned
+    int input_f32;                    // pages hold fp32 values (not BF16)
     Group groups[kMaxGroups];
 };
 
@@ -115,6 +115,7 @@ struct MinMaxParams {
     uint32_t epoch;
     uint32_t chunks_per_job;          // workgroups per job
     int num_groups;
+    int input_f32;                    // fp32 pages: 32-bit keys, NaN marked
     Group groups[kMaxGroups];         // first_tile is the first chunk
 };
 
@@ -133,6 +134,7 @@ struct DecompressParams {
     int dst_kind;
     int rate0_zero;                   // 1: write +0.0 for rate-0 blocks
     int aligned16;                    // every destination base 16B aligned
+    int output_f32;                   // write fp32 values (kDstLinear only)
     uint64_t dests_per_page;
     uint64_t elements_per_dest;
     // Persistent decoder runs balanced by bytes moved: each tile of group

@@ -260,6 +260,29 @@ __device__ __forceinline__ float relative_bound(float eps, uint32_t kmin,
     return eps * range;
 }
 
+// fp32 order keys: key32 = sign ? ~bits : bits | 0x80000000 for a non-NaN
+// value (monotone in the value); kKey32Nan marks "a NaN was seen" in the
+// max word (it exceeds key32(+inf) = 0xFF800000).
+constexpr uint32_t kKey32Nan = 0xFFFFFFFFu;
+__device__ __forceinline__ uint32_t key32(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key32_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// The fp32 single-page bound of cuszp_wrapper.cpp:249-257 and :371-377:
+// at::aminmax over the page (a NaN anywhere makes min and max NaN), then
+// range = max - min, raised to 1e-6f when below it, eb = eps * range.
+__device__ __forceinline__ float relative_bound_f32(float eps, uint32_t kmin,
+                                                    uint32_t kmax) {
+    if (kmax == kKey32Nan) return __uint_as_float(0x7FC00000u);
+    float range = key32_value(kmax) - key32_value(kmin);
+    if (range < 1e-6f) range = 1e-6f;
+    return eps * range;
+}
+
 // ---- layer-index gather ----------------------------------------------------
 
 // selected_bf16_source_index (cu:33-50) for an arbitrary logical index.
@@ -403,6 +426,31 @@ __device__ __forceinline__ void load_block_wave(
         return;
     }
     load_block(g, in, tile_first_elem, elem_in_tile, count, aligned16, d, bad);
+}
+
+// The 32 fp32 values of a block starting at element e0 of a contiguous page
+// (values at or past `count` read as 0): eight 16-byte loads when the block
+// is whole and the page 16-byte aligned, else one value at a time.
+__device__ __forceinline__ void load_block_f32(const float* in, uint64_t e0,
+                                               uint32_t count, bool aligned16,
+                                               uint32_t* d) {
+    if (count == kBlockElems && aligned16) {
+        const g_u32x4* p = (const g_u32x4*)to_global(in + e0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const u32x4 v = p[i];
+            d[4 * i + 0] = v.x;
+            d[4 * i + 1] = v.y;
+            d[4 * i + 2] = v.z;
+            d[4 * i + 3] = v.w;
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < kBlockElems; ++i) d[i] = 0;
+    const __attribute__((address_space(1))) uint32_t* g =
+        (const __attribute__((address_space(1))) uint32_t*)(in + e0);
+    for (uint32_t v = 0; v < count; ++v) d[v] = g[v];
 }
 
 // ---- workgroup scan + decoupled look-back ---------------------------------
@@ -604,13 +652,20 @@ __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t* w,
     }
 }
 
-// Quantized element v of a block held as 16 packed BF16 pairs; elements at
-// or past `count` quantize to 0 (cu:200-211).
-template <int kQuant, bool kFull>
+// Value v of a block: 16 packed BF16 pairs (kIn = 0) or 32 fp32 words
+// (kIn = 1).
+template <int kIn>
+__device__ __forceinline__ float elem_value(const uint32_t* d, int v) {
+    if (kIn) return __uint_as_float(d[v]);
+    return (v & 1) ? bf16_hi(d[v >> 1]) : bf16_lo(d[v >> 1]);
+}
+
+// Quantized element v of a block; elements at or past `count` quantize to 0
+// (cu:200-211).
+template <int kQuant, bool kFull, int kIn = 0>
 __device__ __forceinline__ int32_t quant_elem(const uint32_t* d, int v,
                                               uint32_t count, float recip) {
-    const float x = (v & 1) ? bf16_hi(d[v >> 1]) : bf16_lo(d[v >> 1]);
-    const int32_t q = quantize<kQuant>(x, recip);
+    const int32_t q = quantize<kQuant>(elem_value<kIn>(d, v), recip);
     return (kFull || (uint32_t)v < count) ? q : 0;
 }
 
@@ -620,14 +675,14 @@ __device__ __forceinline__ uint32_t magnitude(int32_t q) {
 
 // Rows of low fields ((|q| << 1) | sign) and the OR of all |q| (the rate is
 // its bit length, cu:221-222).
-template <int kQuant, bool kFull>
+template <int kQuant, bool kFull, int kIn = 0>
 __device__ __forceinline__ void build_rows_lo(const uint32_t* d, uint32_t count,
                                               float recip, uint32_t* P,
                                               uint32_t& orv) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-        const int32_t q0 = quant_elem<kQuant, kFull>(d, row_lo_elem(k), count, recip);
-        const int32_t q1 = quant_elem<kQuant, kFull>(d, row_hi_elem(k), count, recip);
+        const int32_t q0 = quant_elem<kQuant, kFull, kIn>(d, row_lo_elem(k), count, recip);
+        const int32_t q1 = quant_elem<kQuant, kFull, kIn>(d, row_hi_elem(k), count, recip);
         const uint32_t m0 = magnitude(q0), m1 = magnitude(q1);
         orv |= m0 | m1;
         P[k] = field_lo(m0, (uint32_t)q0 >> 31) | (field_lo(m1, (uint32_t)q1 >> 31) << 16);
@@ -671,20 +726,22 @@ __device__ __forceinline__ void build_rows_hi_chained(const uint32_t* d, float r
 }
 
 // Rows of high fields (|q| >> 15), for rates above 15.
-template <int kQuant, bool kFull>
+template <int kQuant, bool kFull, int kIn = 0>
 __device__ __forceinline__ void build_rows_hi(const uint32_t* d, uint32_t count,
                                               float recip, uint32_t* P) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-        const uint32_t m0 = magnitude(quant_elem<kQuant, kFull>(d, row_lo_elem(k), count, recip));
-        const uint32_t m1 = magnitude(quant_elem<kQuant, kFull>(d, row_hi_elem(k), count, recip));
+        const uint32_t m0 = magnitude(quant_elem<kQuant, kFull, kIn>(d, row_lo_elem(k), count, recip));
+        const uint32_t m1 = magnitude(quant_elem<kQuant, kFull, kIn>(d, row_hi_elem(k), count, recip));
         P[k] = field_hi(m0) | (field_hi(m1) << 16);
     }
 }
 
 // ---- encoder ---------------------------------------------------------------
 
-template <int kQuant>
+// kIn = 0: BF16 pages (any bound mode, layer maps); kIn = 1: contiguous
+// fp32 pages (absolute or pre-pass bound), the single-page fp32 API.
+template <int kQuant, int kIn>
 __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     __shared__ uint32_t s_tile;
     __shared__ uint32_t s_wave[kThreads / 64];
@@ -719,12 +776,24 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
         b < nb ? (uint32_t)(n - e0 < kBlockElems ? n - e0 : kBlockElems) : 0u;
 
     uint32_t bad = 0;
-    uint32_t d[16];
-    load_block_wave(g, J.in, tile_first, (uint32_t)tid * kBlockElems, count,
-                    p.aligned16 != 0, d, &bad, &s_stage[wave][0]);
+    uint32_t d[kIn ? kBlockElems : kBlockElems / 2];
+    if constexpr (kIn)
+        load_block_f32(reinterpret_cast<const float*>(J.in), e0, count,
+                       p.aligned16 != 0, d);
+    else
+        load_block_wave(g, J.in, tile_first, (uint32_t)tid * kBlockElems, count,
+                        p.aligned16 != 0, d, &bad, &s_stage[wave][0]);
 
     float eb = J.eps;
-    if (p.bound_mode != kBoundAbsolute) {
+    if constexpr (kIn) {
+        if (p.bound_mode != kBoundAbsolute) {  // pre-pass words (32-bit keys)
+            const unsigned long long wmax = p.job_minmax[2 * job];
+            const unsigned long long wmin = p.job_minmax[2 * job + 1];
+            if ((uint32_t)(wmax >> 32) != p.epoch || (uint32_t)(wmin >> 32) != p.epoch)
+                bad |= 2;
+            eb = relative_bound_f32(J.eps, 0xFFFFFFFFu - (uint32_t)wmin, (uint32_t)wmax);
+        }
+    } else if (p.bound_mode != kBoundAbsolute) {
         uint32_t kmin, kmax;
         if (p.bound_mode == kBoundFused) {
             block_key_minmax(d, count, kmin, kmax);
@@ -794,9 +863,9 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     uint32_t P[16];
     uint32_t orv = 0;
     if (count == kBlockElems)
-        build_rows_lo<kQuant, true>(d, count, recip, P, orv);
+        build_rows_lo<kQuant, true, kIn>(d, count, recip, P, orv);
     else
-        build_rows_lo<kQuant, false>(d, count, recip, P, orv);
+        build_rows_lo<kQuant, false, kIn>(d, count, recip, P, orv);
     const uint32_t rate = orv ? 32u - (uint32_t)__builtin_clz(orv) : 0u;
     const uint32_t bytes = rate ? 4u + 4u * rate : 0u;
     s_rate[tid] = (uint8_t)rate;
@@ -849,12 +918,16 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
         // Planes 15..30 (rates 16..31): high fields, a second transpose.
         // Rare, so the block is re-read instead of kept in registers.
         uint32_t bad2 = 0;
-        load_block(g, J.in, tile_first, (uint32_t)tid * kBlockElems, count,
-                   p.aligned16 != 0, d, &bad2);
-        if (count == kBlockElems)
-            build_rows_hi<kQuant, true>(d, count, recip, P);
+        if constexpr (kIn)
+            load_block_f32(reinterpret_cast<const float*>(J.in), e0, count,
+                           p.aligned16 != 0, d);
         else
-            build_rows_hi<kQuant, false>(d, count, recip, P);
+            load_block(g, J.in, tile_first, (uint32_t)tid * kBlockElems, count,
+                       p.aligned16 != 0, d, &bad2);
+        if (count == kBlockElems)
+            build_rows_hi<kQuant, true, kIn>(d, count, recip, P);
+        else
+            build_rows_hi<kQuant, false, kIn>(d, count, recip, P);
         transpose16x2(P);
         store_words<16>(dst + 16, P, count_words > 16u ? count_words - 16u : 0u,
                         rmax - 15u);
@@ -1665,6 +1738,10 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
 
 // ---- relative-bound pre-pass (jobs too long for the fused exchange) -------
 
+// kIn = 0: BF16 pages, 16-bit keys, NaN ignored (cu:78-79).  kIn = 1:
+// contiguous fp32 pages, 32-bit keys, a NaN marks the max word (at::aminmax
+// propagates NaN, cuszp_wrapper.cpp:253).
+template <int kIn>
 __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
     __shared__ uint32_t s_min[kThreads / 64];
     __shared__ uint32_t s_max[kThreads / 64];
@@ -1686,11 +1763,25 @@ __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
     const uint32_t count =
         b < nb ? (uint32_t)(n - e0 < kBlockElems ? n - e0 : kBlockElems) : 0u;
     uint32_t bad = 0;
-    uint32_t d[16];
-    load_block(g, J.in, (uint64_t)tile * kTileElems, (uint32_t)tid * kBlockElems,
-               count, false, d, &bad);
     uint32_t kmin, kmax;
-    block_key_minmax(d, count, kmin, kmax);
+    if constexpr (kIn) {
+        uint32_t d[kBlockElems];
+        load_block_f32(reinterpret_cast<const float*>(J.in), e0, count,
+                       ((uintptr_t)J.in & 15u) == 0, d);
+        kmin = 0xFFFFFFFFu;
+        kmax = 0u;
+        for (uint32_t v = 0; v < count; ++v) {
+            const float x = __uint_as_float(d[v]);
+            const uint32_t k = x != x ? kKey32Nan : key32(x);
+            kmax = k > kmax ? k : kmax;
+            if (x == x) kmin = k < kmin ? k : kmin;
+        }
+    } else {
+        uint32_t d[16];
+        load_block(g, J.in, (uint64_t)tile * kTileElems, (uint32_t)tid * kBlockElems,
+                   count, false, d, &bad);
+        block_key_minmax(d, count, kmin, kmax);
+    }
     kmin = wave_min(kmin);
     kmax = wave_max(kmax);
     if (lane == 0) {
@@ -1707,8 +1798,9 @@ __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
         const unsigned long long tag = (unsigned long long)p.epoch << 32;
         __hip_atomic_fetch_max(&p.job_minmax[2 * job], tag | kmax,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t key_max = kIn ? 0xFFFFFFFFu : 0xFFFFu;
         __hip_atomic_fetch_max(&p.job_minmax[2 * job + 1],
-                               tag | (0xFFFFu - kmin), __ATOMIC_RELAXED,
+                               tag | (key_max - kmin), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
     if (bad) flag_error(p.error, p.host_ctl, kErrLayerIndex);
@@ -1865,6 +1957,68 @@ __device__ __forceinline__ void decode_block(const uint8_t* in, uint64_t base,
     }
 }
 
+// One block of stream words -> 32 fp32 values y = fl(fl(q * eb) * 2)
+// (cu:535-538 without the BF16 rounding; zeros where rate is 0): the low
+// fields ((|q| << 1) | sign) of words 0..15 and, for rates above 15, the
+// high fields |q| >> 15 of words 16..31, both by the transpose.
+__device__ __forceinline__ void decode_block_f32(const uint8_t* in, uint64_t base,
+                                                 uint32_t rate, uint32_t rmax,
+                                                 float eb, uint32_t* out) {
+    if (rmax == 0) {
+#pragma unroll
+        for (int i = 0; i < kBlockElems; ++i) out[i] = 0;
+        return;
+    }
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(in + base);
+    const uint32_t count_words = rate ? rate + 1u : 0u;
+    uint32_t L[16], H[16];
+    load_words<16>(src, L, count_words < 16u ? count_words : 16u,
+                   rmax < 15u ? rmax + 1u : 16u);
+    transpose16x2(L);
+    if (rmax > 15u) {
+        load_words<16>(src + 16, H, count_words > 16u ? count_words - 16u : 0u,
+                       rmax - 15u);
+        transpose16x2(H);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) H[k] = 0;
+    }
+    const bool eb2_ok = eb >= FLT_MIN && eb <= FLT_MAX / 2;  // uniform
+    const float eb2 = eb * 2.0f;
+#pragma unroll
+    for (int v = 0; v < kBlockElems; ++v) {
+        const int k = (v & 15) ^ 7, sh = v < 16 ? 0 : 16;
+        const uint32_t lo = (L[k] >> sh) & 0xFFFFu;
+        const uint32_t m = (lo >> 1) | (((H[k] >> sh) & 0xFFFFu) << 15);
+        const uint32_t sg = lo & 1u;
+        const int32_t q = (int32_t)((m ^ (0u - sg)) + sg);
+        // fl(fl(q*eb)*2) == fl(q*(2eb)) for FLT_MIN <= eb <= FLT_MAX/2
+        const float y = eb2_ok ? (float)q * eb2 : ((float)q * eb) * 2.0f;
+        out[v] = rate ? __float_as_uint(y) : 0u;
+    }
+}
+
+// Writes 32 decoded fp32 values (eight 16-byte stores when whole and
+// aligned, else value by value).
+__device__ __forceinline__ void store_block_f32(float* dst, const uint32_t* out,
+                                                uint32_t count) {
+    if (count == kBlockElems && ((uintptr_t)dst & 15u) == 0) {
+        g_u32x4* p = (g_u32x4*)to_global(reinterpret_cast<uint32_t*>(dst));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            u32x4 v;
+            v.x = out[4 * i + 0];
+            v.y = out[4 * i + 1];
+            v.z = out[4 * i + 2];
+            v.w = out[4 * i + 3];
+            p[i] = v;
+        }
+        return;
+    }
+    g_u32* g = to_global(reinterpret_cast<uint32_t*>(dst));
+    for (uint32_t v = 0; v < count; ++v) g[v] = out[v];
+}
+
 // Destination of this thread's decoded block when its `count` values go to
 // one contiguous run (cu:539-606: contiguous page, multi-destination split,
 // or layer-indexed position in the full page); nullptr when they do not (or
@@ -2016,7 +2170,9 @@ __device__ __forceinline__ void store_decoded(const DecompressParams& p,
     if (write) store_block_lane<kDst>(p, g, J, job, tile, tid, e0, count, out, err);
 }
 
-template <int kDst>
+// kOut = 0: BF16 values to any destination kind; kOut = 1: fp32 values to
+// contiguous per-job outputs (the single-page fp32 API).
+template <int kDst, int kOut>
 __global__ __launch_bounds__(kThreads) void decompress_kernel(
     DecompressParams p) {
     __shared__ uint32_t s_tile;
@@ -2077,12 +2233,19 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     // Unpack (cu:496-538): stream words back to fields, then values
     // y = bf16_rne((float(q) * eb) * 2) (cu:535-538).
     const uint32_t rmax = wave_max(rate);
-    uint32_t out[16];
-    decode_block(J.in, base, rate, rmax, J.eb, out, s_park);
-    store_decoded<kDst>(p, g, J, job, tile, tid, e0, count,
-                        count != 0 && (rate != 0 || p.rate0_zero),
-                        wave_run_dst<kDst>(p, g, J, job, tile, wave), out,
-                        &s_park[0][64 * wave], err);
+    if constexpr (kOut) {
+        uint32_t out[kBlockElems];
+        decode_block_f32(J.in, base, rate, rmax, J.eb, out);
+        if (count != 0 && (rate != 0 || p.rate0_zero))
+            store_block_f32(reinterpret_cast<float*>(J.dst) + e0, out, count);
+    } else {
+        uint32_t out[16];
+        decode_block(J.in, base, rate, rmax, J.eb, out, s_park);
+        store_decoded<kDst>(p, g, J, job, tile, tid, e0, count,
+                            count != 0 && (rate != 0 || p.rate0_zero),
+                            wave_run_dst<kDst>(p, g, J, job, tile, wave), out,
+                            &s_park[0][64 * wave], err);
+    }
     if (err) flag_error(p.error, p.host_ctl, err);
 }
 
@@ -2266,10 +2429,16 @@ static void launch(void (*kernel)(Args...), uint32_t grid, hipStream_t stream,
 
 hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
                            hipEvent_t start, hipEvent_t stop) {
-    if (p.quantizer)
-        launch(compress_kernel<1>, p.total_tiles, stream, start, stop, p);
-    else
-        launch(compress_kernel<0>, p.total_tiles, stream, start, stop, p);
+    if (p.input_f32) {
+        if (p.quantizer)
+            launch(compress_kernel<1, 1>, p.total_tiles, stream, start, stop, p);
+        else
+            launch(compress_kernel<0, 1>, p.total_tiles, stream, start, stop, p);
+    } else if (p.quantizer) {
+        launch(compress_kernel<1, 0>, p.total_tiles, stream, start, stop, p);
+    } else {
+        launch(compress_kernel<0, 0>, p.total_tiles, stream, start, stop, p);
+    }
     return hipGetLastError();
 }
 
@@ -2285,7 +2454,10 @@ hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
 
 hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
                          hipStream_t stream, hipEvent_t start) {
-    launch(minmax_kernel, grid, stream, start, nullptr, p);
+    if (p.input_f32)
+        launch(minmax_kernel<1>, grid, stream, start, nullptr, p);
+    else
+        launch(minmax_kernel<0>, grid, stream, start, nullptr, p);
     return hipGetLastError();
 }
 
@@ -2319,15 +2491,19 @@ int decompress_resident_workgroups(int device) {
 
 hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
                              hipEvent_t start, hipEvent_t stop) {
+    if (p.output_f32) {
+        launch(decompress_kernel<kDstLinear, 1>, p.total_tiles, stream, start, stop, p);
+        return hipGetLastError();
+    }
     switch (p.dst_kind) {
     case kDstMulti:
-        launch(decompress_kernel<kDstMulti>, p.total_tiles, stream, start, stop, p);
+        launch(decompress_kernel<kDstMulti, 0>, p.total_tiles, stream, start, stop, p);
         break;
     case kDstIndexed:
-        launch(decompress_kernel<kDstIndexed>, p.total_tiles, stream, start, stop, p);
+        launch(decompress_kernel<kDstIndexed, 0>, p.total_tiles, stream, start, stop, p);
         break;
     default:
-        launch(decompress_kernel<kDstLinear>, p.total_tiles, stream, start, stop, p);
+        launch(decompress_kernel<kDstLinear, 0>, p.total_tiles, stream, start, stop, p);
         break;
     }
     return hipGetLastError();
@@ -2337,7 +2513,7 @@ int compress_resident_workgroups(int device, bool pipelined) {
     int per_cu = 0;
     const void* fn = pipelined
         ? reinterpret_cast<const void*>(compress_persistent_kernel<0>)
-        : reinterpret_cast<const void*>(compress_kernel<0>);
+        : reinterpret_cast<const void*>(compress_kernel<0, 0>);
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &per_cu, fn, pipelined ? kEncThreads : kThreads, 0) != hipSuccess)
         per_cu = 1;

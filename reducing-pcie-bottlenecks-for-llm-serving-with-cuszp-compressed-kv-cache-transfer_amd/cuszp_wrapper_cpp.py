@@ -19,9 +19,10 @@ call runs on ``torch.cuda.current_stream()`` (the reference captures
 the sizes are on the host, decompress calls only enqueue.
 
 The single-page fp32 entry points (``compress``, ``compress_batch_fixed``,
-``decompress``, ``decompress_batch``) belong to the upstream cuSZp fp32
-kernels, which this codec does not implement; they report failure (the
-connector then raises or falls back, as it does on any codec failure).
+``decompress``, ``decompress_batch``) run the same kernels with fp32 loads and
+stores in fixed mode (the reference uses upstream cuSZp's fp32 kernels, whose
+stream layout the batched BF16 codec shares); upstream's plain/outlier modes
+are not provided and report failure.
 """
 
 from __future__ import annotations
@@ -502,27 +503,132 @@ class CuSZpWrapper:
             return False
         return True
 
-    # ---- single-page fp32 API (upstream cuSZp kernels; not implemented) ---
+    # ---- single-page fp32 API (fixed mode) ------------------------------
+    # The reference runs upstream cuSZp's fp32 kernels here
+    # (cuszp_fastpath.cu:5-64); the stream layout is the batched BF16 one
+    # (cuszp_batched_fixed.cu:52-54), so the same HIP kernels serve it with
+    # fp32 loads and stores.  The plain/outlier modes of upstream cuSZp are
+    # not provided: those calls report failure.
+
+    def _fp32_ok(self, t: torch.Tensor) -> bool:
+        # The reference reads data_ptr() as a dense float array without
+        # checking; other dtypes or layouts are refused here instead.
+        return (self._on_device(t) and t.dtype == torch.float32
+                and t.is_contiguous() and t.numel() > 0)
 
     def compress(self, input_tensor, compressed_buffer, eps_override=-1.0):
-        """pybind11_bindings.cpp:49-64 (upstream fp32 codec)."""
-        print("Error: fp32 single-page cuSZp compress is not provided by this "
-              "codec", file=sys.stderr)
-        return (False, compressed_buffer, 0, 0.0)
+        """pybind11_bindings.cpp:49-64 -> cuszp_wrapper.cpp:216-325.  Returns
+        (ok, buffer, size, actual_error_bound); a buffer smaller than
+        estimate_compressed_buffer_size(nbytes) is replaced by a new one, as
+        in the reference (:229-237)."""
+        if not input_tensor.is_cuda:
+            print("Error: Input tensor must be on GPU", file=sys.stderr)
+            return (False, compressed_buffer, 0, 0.0)
+        if not self._fixed_mode() or not self._fp32_ok(input_tensor):
+            print("Error: cuSZp compression failed (fp32 fixed 1D only)",
+                  file=sys.stderr)
+            return (False, compressed_buffer, 0, 0.0)
+        n = input_tensor.numel()
+        # estimate(nbytes) = 8n, raised to the worst-case stream for tiny
+        # inputs (a 1024-byte header per 32 768 values), which 8n does not
+        # cover below 147 values.
+        estimated = max(self.estimate_compressed_buffer_size(4 * n),
+                        kvszp.header_bytes(n) + 128 * ((n + 31) // 32))
+        if (compressed_buffer.numel() * compressed_buffer.element_size()
+                < estimated or not self._on_device(compressed_buffer)
+                or not compressed_buffer.is_contiguous()):
+            compressed_buffer = torch.empty(estimated, dtype=torch.uint8,
+                                            device=input_tensor.device)
+        size = ctypes.c_uint64()
+        bound = ctypes.c_float()
+        rc = self._ctx.compress_f32(
+            input_tensor.data_ptr(), n, compressed_buffer.data_ptr(),
+            compressed_buffer.numel() * compressed_buffer.element_size(),
+            _f32(eps_override), _stream_handle(self._device_id),
+            ctypes.byref(size), ctypes.byref(bound))
+        if rc != kvszp.OK:
+            _report("cuSZp compression failed")
+            return (False, compressed_buffer, 0, 0.0)
+        return (True, compressed_buffer, int(size.value), float(bound.value))
 
     def compress_batch_fixed(self, input_tensors, compressed_buffers,
                              eps_overrides):
-        """pybind11_bindings.cpp:65-82 (upstream fp32 codec)."""
-        return (False, [], [])
+        """pybind11_bindings.cpp:65-82 -> cuszp_wrapper.cpp:327-429."""
+        batch = len(input_tensors)
+        if (batch == 0 or len(compressed_buffers) != batch
+                or (eps_overrides and len(eps_overrides) != batch)
+                or not self._fixed_mode()):
+            return (False, [], [])
+        n = input_tensors[0].numel()
+        capacity = self.estimate_compressed_buffer_size(4 * n)
+        for inp, out in zip(input_tensors, compressed_buffers):
+            if (not self._fp32_ok(inp) or inp.numel() != n
+                    or not self._on_device(out) or out.dtype != torch.uint8
+                    or not out.is_contiguous() or out.numel() < capacity):
+                return (False, [], [])
+        sizes = (ctypes.c_uint64 * batch)()
+        bounds = (ctypes.c_float * batch)()
+        rc = self._ctx.compress_batch_f32(
+            kvszp.ptr_array([t.data_ptr() for t in input_tensors]),
+            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
+            kvszp.u64_array([t.numel() for t in compressed_buffers]),
+            self._eps_array(eps_overrides, batch), batch, n,
+            _stream_handle(self._device_id), sizes, bounds)
+        return self._finish_compress(rc, batch, sizes, bounds,
+                                     "cuSZp fixed batch compression failed")
 
     def decompress(self, compressed_buffer, compressed_size, output_tensor,
                    actual_error_bound):
-        """pybind11_bindings.cpp:164-173 (upstream fp32 codec)."""
-        print("Error: fp32 single-page cuSZp decompress is not provided by "
-              "this codec", file=sys.stderr)
-        return False
+        """pybind11_bindings.cpp:164-173 -> cuszp_wrapper.cpp:870-943: decodes
+        output_tensor.numel() fp32 values; enqueue only."""
+        if not compressed_buffer.is_cuda or not output_tensor.is_cuda:
+            print("Error: Both compressed buffer and output tensor must be on "
+                  "GPU", file=sys.stderr)
+            return False
+        if (not self._fixed_mode() or not self._fp32_ok(output_tensor)
+                or not self._on_device(compressed_buffer)
+                or int(compressed_size) == 0):
+            print("Error: cuSZp decompression failed (fp32 fixed 1D only)",
+                  file=sys.stderr)
+            return False
+        rc = self._ctx.decompress_f32(
+            compressed_buffer.data_ptr(), int(compressed_size),
+            output_tensor.data_ptr(), output_tensor.numel(),
+            _f32(actual_error_bound), _stream_handle(self._device_id))
+        if rc != kvszp.OK:
+            _report("cuSZp fast decompression failed")
+            return False
+        return True
 
     def decompress_batch(self, compressed_buffers, compressed_sizes,
                          output_tensors, actual_error_bounds):
-        """pybind11_bindings.cpp:174-189 (upstream fp32 codec)."""
-        return False
+        """pybind11_bindings.cpp:174-189 -> cuszp_wrapper.cpp:944-1033: page i
+        to output_tensors[i] (fp32, any length); enqueue only."""
+        batch = len(compressed_buffers)
+        if batch == 0:
+            return True
+        if (len(compressed_sizes) != batch or len(output_tensors) != batch
+                or len(actual_error_bounds) != batch):
+            print("Error: cuSZp batch metadata lengths differ", file=sys.stderr)
+            return False
+        if not self._fixed_mode():
+            print("Error: cuSZp batch fast path requires 1D f32 fixed mode",
+                  file=sys.stderr)
+            return False
+        for comp, size, out in zip(compressed_buffers, compressed_sizes,
+                                   output_tensors):
+            if (not self._on_device(comp) or not self._fp32_ok(out)
+                    or int(size) == 0):
+                print("Error: invalid tensor in cuSZp batch", file=sys.stderr)
+                return False
+        rc = self._ctx.decompress_batch_f32(
+            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
+            kvszp.u64_array([int(s) for s in compressed_sizes]),
+            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
+            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
+            kvszp.u64_array([t.numel() for t in output_tensors]),
+            _stream_handle(self._device_id))
+        if rc != kvszp.OK:
+            _report("cuSZp batched decompression failed")
+            return False
+        return True

@@ -61,6 +61,14 @@ EXPORTS = [
      [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
     ("kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups", _i,
      [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
+    ("kvszp_compress_fixed_f32", _i,
+     [_vp, _vp, _sz, _vp, ctypes.c_uint64, ctypes.c_float, _vp, _vp, _vp]),
+    ("kvszp_compress_batch_fixed_f32", _i,
+     [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp]),
+    ("kvszp_decompress_fixed_f32", _i,
+     [_vp, _vp, ctypes.c_uint64, _vp, _sz, ctypes.c_float, _vp]),
+    ("kvszp_decompress_batch_fixed_f32", _i,
+     [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
     ("kvszp_synchronize", _i, [_vp, _vp]),
     ("kvszp_enable_timing", _i, [_vp, _i]),
     ("kvszp_drain_timing", _i, [_vp, _vp, _vp, _vp, _vp]),
@@ -239,6 +247,29 @@ class Context:
             self.handle, compressed, sizes, bounds, batch, destinations,
             layer_indices, selected_layers, group_sizes, num_groups,
             prefix_count, source_layers, elements_per_layer, stream)
+
+    def compress_f32(self, input_ptr, n, output_ptr, capacity, eps_override,
+                     stream, size_out, bound_out) -> int:
+        return self._lib.kvszp_compress_fixed_f32(
+            self.handle, input_ptr, n, output_ptr, capacity, eps_override,
+            stream, size_out, bound_out)
+
+    def compress_batch_f32(self, inputs, outputs, capacities, eps, batch, n,
+                           stream, sizes_out, bounds_out) -> int:
+        return self._lib.kvszp_compress_batch_fixed_f32(
+            self.handle, inputs, outputs, capacities, eps, batch, n, stream,
+            sizes_out, bounds_out)
+
+    def decompress_f32(self, compressed_ptr, size, output_ptr, n, eb,
+                       stream) -> int:
+        return self._lib.kvszp_decompress_fixed_f32(
+            self.handle, compressed_ptr, size, output_ptr, n, eb, stream)
+
+    def decompress_batch_f32(self, compressed, sizes, bounds, batch, outputs,
+                             numels, stream) -> int:
+        return self._lib.kvszp_decompress_batch_fixed_f32(
+            self.handle, compressed, sizes, bounds, batch, outputs, numels,
+            stream)
 
     def synchronize(self, stream) -> int:
         return self._lib.kvszp_synchronize(self.handle, stream)

@@ -553,3 +553,58 @@ def test_both_decoder_schedules_match_oracle(cpp, oracle, persistent, rate0,
         want = oracle.decompress_contiguous(bufs[i][:sizes[i]].cpu().numpy(), n,
                                             bounds[i], rate0, pre.copy())
         assert np.array_equal(got[i * n:(i + 1) * n], want), f"page {i}"
+
+
+def test_indexed_groups_beyond_sixteen_groups(cpp, oracle):
+    """One REL bound per Qwen2.5-1.5B layer: 28 layer groups of 8 pages in
+    one compress_batch_fixed_bf16_indexed_groups call (the reference takes
+    any number of groups, cuszp_wrapper.cpp:683-868) and one grouped
+    restore; byte-exact against the oracle."""
+    import kv_synth
+
+    shape = kv_synth.QWEN25_1P5B_4K
+    pages = kv_synth.paged_kv(shape, seed=4, device=DEV, tokens=128)  # 8 pages
+    epl, layers = shape.elements_per_layer, shape.layers
+    bits = u16(pages)
+    eps_of = [1e-5 if l in kv_synth.QWEN15B_SENSITIVE_LAYERS else 1e-4 * (1 + l % 3)
+              for l in range(layers)]
+    inputs, bufs, eps, idx_t, counts, jobs = [], [], [], [], [], []
+    n = 2 * epl
+    for l in range(layers):
+        idx_t.append(torch.tensor([l], dtype=torch.long, device=DEV))
+        counts.append(pages.shape[0])
+        for p in range(pages.shape[0]):
+            inputs.append(pages[p])
+            eps.append(eps_of[l])
+            jobs.append((l, p))
+        bufs.extend(buffers(cpp, pages.shape[0], n))
+    w = make(cpp)
+    ok, sizes, bounds = w.compress_batch_fixed_bf16_indexed_groups(
+        inputs, bufs, idx_t, counts, 2, layers, epl, eps)
+    assert ok and len(sizes) == layers * pages.shape[0]
+    for k, (l, p) in enumerate(jobs):
+        eb = oracle.relative_bound(bits[p], n, eps_of[l], [l], layers, epl)
+        assert np.float32(bounds[k]) == np.float32(eb), (l, p)
+        want = oracle.compress_page(bits[p], n, float(eb), [l], layers, epl)
+        assert sizes[k] == want.size and np.array_equal(
+            bufs[k][:sizes[k]].cpu().numpy(), want), (l, p)
+    # restore every layer group of every page in one grouped call
+    dest = torch.full((len(jobs), pages.shape[1]), -2.0, dtype=torch.bfloat16, device=DEV)
+    assert w.decompress_batch_fixed_bf16_indexed_scatter_groups(
+        bufs, sizes, list(dest), idx_t, counts, 2, layers, epl, bounds)
+    assert w.synchronize()
+    got = u16(dest)
+    for k, (l, p) in enumerate(jobs):
+        want = u16(torch.full((pages.shape[1],), -2.0, dtype=torch.bfloat16))
+        oracle.decompress_indexed(bufs[k][:sizes[k]].cpu().numpy(), n, bounds[k],
+                                  want, [l], layers, epl)
+        assert np.array_equal(got[k], want), (l, p)
+    # into shared pages: all 28 groups of a page land in the same page
+    shared = torch.zeros_like(pages)
+    dests = [shared[p] for (_, p) in jobs]
+    assert w.decompress_batch_fixed_bf16_indexed_scatter_groups(
+        bufs, sizes, dests, idx_t, counts, 2, layers, epl, bounds)
+    assert w.synchronize()
+    err = (shared.float() - pages.float()).abs().view(pages.shape[0], 2, layers, epl)
+    for k, (l, p) in enumerate(jobs):
+        assert float(err[p, :, l].max()) <= 2 * bounds[k] + 1e-7

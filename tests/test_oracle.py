@@ -370,3 +370,94 @@ def test_int8_codec_matches_torch_formula(oracle):
     y_t = (q_t.to(torch.float32) * float(scale_t)).to(torch.bfloat16)
     y = oracle.int8_decode(q, scale)
     assert np.array_equal(y, y_t.view(torch.int16).numpy().view(np.uint16))
+
+
+# ---- fp32 single-page path (CuSZpWrapper::compress / decompress) -------------
+
+def _aminmax_bound(x: np.ndarray, eps: float) -> np.float32:
+    """cuszp_wrapper.cpp:249-257 through torch's own aminmax (NaN propagates)."""
+    mn, mx = torch.aminmax(torch.from_numpy(x))
+    rng = np.float32(mx.item()) - np.float32(mn.item())
+    if rng < np.float32(1e-6):
+        rng = np.float32(1e-6)
+    return np.float32(np.float32(eps) * rng)
+
+
+@pytest.mark.parametrize("case", ["randn", "const", "nan", "infs", "pos_inf",
+                                  "signed_zero", "tiny"])
+def test_relative_bound_f32_matches_torch_aminmax(oracle, case):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(5000) * 3).astype(np.float32)
+    if case == "const":
+        x[:] = 2.5
+    elif case == "nan":
+        x[1234] = np.nan
+    elif case == "infs":
+        x[10], x[20] = np.inf, -np.inf
+    elif case == "pos_inf":
+        x[:] = np.inf
+    elif case == "signed_zero":
+        x[:] = 0.0
+        x[::2] = -0.0
+    elif case == "tiny":
+        x = (x * 1e-9).astype(np.float32)
+    want = _aminmax_bound(x, 1e-4)
+    got = np.float32(oracle.relative_bound_f32(x, 1e-4))
+    if np.isnan(want):
+        assert np.isnan(got)
+    else:
+        assert got == want
+
+
+def test_f32_stream_hand_example(oracle):
+    # x = [0.75, -1.0000001, 3.0, 0...], eb = 0.5 -> recip = 1:
+    # q = [1, -1, 3]: 0.75+0.5 -> 1; v = -1.0000001 < -0.5 gives s = 1 and
+    # t = -0.5000001 truncates to 0, so q = -1; 3.5 -> 3.  Rate 2.
+    x = np.zeros(40, dtype=np.float32)
+    x[:3] = [0.75, np.float32(-1.0000001), 3.0]
+    s = oracle.compress_page_f32(x, 0.5)
+    assert s.size == 1024 + 4 + 4 * 2
+    assert s[0] == 2 and s[1] == 0 and not s[2:1024].any()
+    assert list(s[1024:1028]) == [0x40, 0, 0, 0]   # element 1 negative
+    assert list(s[1028:1032]) == [0xE0, 0, 0, 0]   # plane 0: elements 0,1,2
+    assert list(s[1032:1036]) == [0x20, 0, 0, 0]   # plane 1: element 2 (q=3)
+    y = oracle.decompress_f32(s, 40, 0.5)
+    assert list(y[:4]) == [1.0, -1.0, 3.0, 0.0] and not y[4:].any()
+
+
+@pytest.mark.parametrize("n", [40, 36864, 70001])
+def test_f32_encoder_on_widened_bf16_equals_bf16_encoder(oracle, n):
+    """A BF16 page widened to fp32 has the same values, so with the same
+    bound the fp32 path must write the BF16 path's stream."""
+    rng = np.random.default_rng(n)
+    bits = bf16_bits(rng.standard_normal(n) * 2)
+    x = bits_to_f32(bits)
+    eb = np.float32(oracle.relative_bound(bits, n, 1e-4))
+    assert eb == np.float32(oracle.relative_bound_f32(x, 1e-4))
+    assert np.array_equal(oracle.compress_page_f32(x, float(eb)),
+                          oracle.compress_page(bits, n, float(eb)))
+
+
+def test_f32_decoder_rounded_is_bf16_decoder(oracle):
+    """torch's fp32 -> BF16 rounding of the fp32 decode is the BF16
+    decoders' output (cu:535-538 differs only by that rounding)."""
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(50000) * 5).astype(np.float32)
+    x[:3000] = 0.0                                  # rate-0 blocks
+    eb = oracle.relative_bound_f32(x, 1e-5)
+    s = oracle.compress_page_f32(x, eb)
+    y = oracle.decompress_f32(s, x.size, eb)
+    rounded = torch.from_numpy(y).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(rounded, oracle.decompress_contiguous(s, x.size, eb))
+    assert np.abs(y - x).max() <= 1.01 * eb + 1e-7  # reference tolerance (tests :45)
+
+
+def test_stream_capacity_covers_partial_blocks_at_rate_31(oracle):
+    """One value on a constant page under a relative bound has rate 31: its
+    block takes 4 + 124 bytes whatever the block's length."""
+    for n in (1, 33, 100):
+        x = np.full(n, 2.5, dtype=np.float32)
+        s = oracle.compress_page_f32(x, oracle.relative_bound_f32(x, 1e-4))
+        nb = (n + 31) // 32
+        assert s.size == oracle.header_bytes(n) + 128 * nb == oracle.max_stream_bytes(n)
+        assert list(s[:nb]) == [31] * nb
