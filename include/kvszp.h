@@ -98,6 +98,23 @@ int kvszp_compress_batch_fixed_bf16(
     size_t num_elements, kvszp_stream_t stream, uint64_t* sizes_out,
     float* bounds_out);
 
+/* kvszp_compress_batch_fixed_bf16 for callers that cannot allocate memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, checks and
+ * results as kvszp_compress_batch_fixed_bf16, but the call allocates
+ * nothing: the encoder's device state (look-back and min/max words, job
+ * table) lives in one file-scope device array per GPU of about 1.2 MiB,
+ * held until the process ends, and its pinned host areas are set up by
+ * kvszp_create.  Limits: at most 4096 pages and 65536 tiles of 8192 values
+ * (512 Mi values) per call; larger calls fail with KVSZP_EINVAL.  All
+ * contexts on a GPU share that array: calls that overlap in time on one GPU
+ * (two host threads, or two streams) race and must not be issued. */
+int kvszp_compress_batch_fixed_bf16_noalloc(
+    kvszp_ctx* ctx, const void* const* inputs, void* const* outputs,
+    const uint64_t* capacities, const float* eps_overrides, size_t batch,
+    size_t num_elements, kvszp_stream_t stream, uint64_t* sizes_out,
+    float* bounds_out);
+
 /* Replaces CuSZpWrapper::compress_batch_fixed_bf16_indexed,
  * cuszp_wrapper.cpp:548-681 (pybind11_bindings.cpp:104-132).  Page i is
  * read as view(prefix_count, source_layers, elements_per_layer) and the

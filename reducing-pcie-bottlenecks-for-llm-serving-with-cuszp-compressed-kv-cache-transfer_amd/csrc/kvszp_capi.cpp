@@ -22,6 +22,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -103,6 +104,11 @@ struct kvszp_ctx {
     uint32_t* host_ctl = nullptr;         // pinned coherent control block
     void* host_results = nullptr;         // pinned coherent sizes + bounds
     size_t host_results_bytes = 0;
+    // No-allocation encoder: the device's scratch array (device address) and
+    // pinned host areas of fixed size, all set up by kvszp_create.
+    unsigned char* scratch = nullptr;
+    CompressJob* noalloc_stage = nullptr;     // kNoAllocMaxJobs job records
+    void* noalloc_results = nullptr;          // kNoAllocMaxJobs sizes + bounds
     // Optional kernel timing: event pairs recorded on the launch stream for
     // the kernel kinds in the mask (bit KVSZP_KERNEL_*).
     int timing = 0;
@@ -731,6 +737,23 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
         kvszp_destroy(c);
         return hip_fail(e, "context setup");
     }
+    // No-allocation entry point: the device's scratch array and the pinned
+    // areas its calls use, so that those calls allocate nothing.
+    {
+        void* sp = nullptr;
+        e = scratch_address(device_id, &sp);
+        if (e == hipSuccess)
+            e = hipHostMalloc(reinterpret_cast<void**>(&c->noalloc_stage),
+                              sizeof(CompressJob) * kNoAllocMaxJobs, hipHostMallocDefault);
+        if (e == hipSuccess)
+            e = hipHostMalloc(&c->noalloc_results, 8ull * kNoAllocMaxJobs,
+                              hipHostMallocCoherent);
+        if (e != hipSuccess) {
+            kvszp_destroy(c);
+            return hip_fail(e, "scratch setup");
+        }
+        c->scratch = static_cast<unsigned char*>(sp);
+    }
     // Tiles of one job wait for each other in the fused relative-bound
     // exchange, so a job may use it only if all its tiles fit on the device
     // at once with a wide margin.
@@ -773,6 +796,8 @@ int kvszp_destroy(kvszp_ctx* c) {
     if (c->control) (void)hipFree(c->control);
     if (c->host_results) (void)hipHostFree(c->host_results);
     if (c->host_ctl) (void)hipHostFree(c->host_ctl);
+    if (c->noalloc_stage) (void)hipHostFree(c->noalloc_stage);
+    if (c->noalloc_results) (void)hipHostFree(c->noalloc_results);
     delete c;
     return KVSZP_OK;
 }
@@ -817,6 +842,153 @@ int kvszp_compress_batch_fixed_bf16(kvszp_ctx* c, const void* const* inputs,
     specs[0] = GroupSpec{num_elements, nullptr, 0, 0, 0, (uint32_t)batch};
     return compress_groups(c, inputs, outputs, capacities, eps_overrides, batch,
                            specs, (hipStream_t)stream, sizes_out, bounds_out);
+}
+
+// Epoch tags of the words in each device's scratch array.  All contexts on
+// a device share the array, so the tags come from one counter per device:
+// no two calls on a device use the same tag, and a wrap clears the tagged
+// words first.
+static std::mutex g_scratch_epoch_mutex;
+static uint32_t g_scratch_epoch[64];
+
+static int scratch_epoch(kvszp_ctx* c, hipStream_t stream, uint32_t* epoch) {
+    std::lock_guard<std::mutex> lock(g_scratch_epoch_mutex);
+    uint32_t& cur = g_scratch_epoch[c->device];
+    if (cur >= kEpochLimit) {
+        hipError_t e = launch_fill_u64(reinterpret_cast<unsigned long long*>(c->scratch),
+                                       kScratchJobs / 8, stream);
+        if (e != hipSuccess) return hip_fail(e, "clearing the scratch words");
+        cur = 0;
+    }
+    *epoch = ++cur;
+    return KVSZP_OK;
+}
+
+int kvszp_compress_batch_fixed_bf16_noalloc(
+    kvszp_ctx* c, const void* const* inputs, void* const* outputs,
+    const uint64_t* capacities, const float* eps_overrides, size_t batch,
+    size_t num_elements, kvszp_stream_t stream_handle, uint64_t* sizes_out,
+    float* bounds_out) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    hipStream_t stream = (hipStream_t)stream_handle;
+    int rc = check_fixed_config(c);
+    if (rc) return rc;
+    if (batch == 0) return fail(KVSZP_EINVAL, "empty batch");
+    if (!inputs || !outputs || !sizes_out || !bounds_out)
+        return fail(KVSZP_EINVAL, "null pointer argument");
+    const uint64_t n = num_elements;
+    if (n == 0 || n > kMaxElements)
+        return fail(KVSZP_EINVAL, "segment of %llu elements unsupported",
+                    (unsigned long long)n);
+    const uint32_t tiles_per_job = (uint32_t)((n + kTileElems - 1) / kTileElems);
+    if (batch > kNoAllocMaxJobs || (uint64_t)tiles_per_job * batch > kNoAllocMaxTiles)
+        return fail(KVSZP_EINVAL,
+                    "no-allocation compress takes at most %u pages and %u tiles of "
+                    "8192 values per call (got %zu pages, %llu tiles)",
+                    kNoAllocMaxJobs, kNoAllocMaxTiles, batch,
+                    (unsigned long long)tiles_per_job * batch);
+    rc = use_device(c);
+    if (rc) return rc;
+    const uint64_t need = std::max<uint64_t>(8ull * n, header_bytes_of(n) + 128ull * ((n + 31) / 32));
+    bool aligned16 = true;
+    for (size_t i = 0; i < batch; ++i) {
+        const uintptr_t in = (uintptr_t)inputs[i], out = (uintptr_t)outputs[i];
+        if (!in || !out) return fail(KVSZP_EINVAL, "null page pointer %zu", i);
+        if (in & 1u) return fail(KVSZP_EINVAL, "input %zu not 2-byte aligned", i);
+        if (out & 3u) return fail(KVSZP_EINVAL, "compressed buffer %zu not 4-byte aligned", i);
+        if (capacities && capacities[i] < need)
+            return fail(KVSZP_EINVAL, "compressed buffer %zu holds %llu bytes, needs %llu", i,
+                        (unsigned long long)capacities[i], (unsigned long long)need);
+        if (in & 15u) aligned16 = false;
+        CompressJob& j = c->noalloc_stage[i];
+        j.in = reinterpret_cast<const uint16_t*>(in);
+        j.out = reinterpret_cast<uint8_t*>(out);
+        j.eps = (eps_overrides && eps_overrides[i] > 0.0f) ? eps_overrides[i]
+                                                          : c->config.error_bound;
+        j.reserved = 0;
+    }
+    // The previous call on this context waited for its kernels, so the
+    // staging records are free; the copy goes into the scratch job table.
+    CompressJob* djobs = reinterpret_cast<CompressJob*>(c->scratch + kScratchJobs);
+    hipError_t e = hipMemcpyAsync(djobs, c->noalloc_stage, batch * sizeof(CompressJob),
+                                  hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D job table)");
+    uint32_t epoch;
+    if ((rc = scratch_epoch(c, stream, &epoch))) return rc;
+
+    const bool relative = c->config.use_relative_error != 0;
+    const bool whole_blocks = (n % kBlockElems) == 0;
+    const uint32_t seq = ++c->seq;
+    CompressParams p;
+    std::memset(&p, 0, sizeof(p));
+    Group& g = p.groups[0];
+    g.n = n;
+    g.first_job = 0;
+    g.first_tile = 0;
+    g.tiles_per_job = tiles_per_job;
+    g.header_bytes = header_bytes_of(n);
+    p.num_groups = 1;
+    const int bound_mode = !relative ? kBoundAbsolute
+                           : (tiles_per_job <= c->fused_tile_limit ? kBoundFused : kBoundPrepass);
+    uint32_t* host_sizes = reinterpret_cast<uint32_t*>(c->noalloc_results);
+    float* host_bounds = reinterpret_cast<float*>(host_sizes + kNoAllocMaxJobs);
+    unsigned long long* words = reinterpret_cast<unsigned long long*>(c->scratch);
+    if (bound_mode == kBoundPrepass) {
+        MinMaxParams m;
+        std::memset(&m, 0, sizeof(m));
+        m.jobs = djobs;
+        m.job_minmax = words + kScratchJobMinMax / 8;
+        m.error = error_word(c);
+        m.host_ctl = c->host_ctl;
+        m.seq = seq;
+        m.epoch = epoch;
+        m.num_groups = 1;
+        m.groups[0] = g;
+        e = launch_minmax(m, tiles_per_job * (uint32_t)batch, stream, nullptr);
+        if (e != hipSuccess) return hip_fail(e, "minmax launch");
+    }
+    p.jobs = djobs;
+    p.tile_state = words + kScratchTileState / 8;
+    p.tile_minmax = words + kScratchTileMinMax / 8;
+    p.job_minmax = words + kScratchJobMinMax / 8;
+    p.host_sizes = host_sizes;
+    p.host_bounds = host_bounds;
+    p.error = error_word(c);
+    p.host_ctl = c->host_ctl;
+    p.seq = seq;
+    p.epoch = epoch;
+    p.total_tiles = tiles_per_job * (uint32_t)batch;
+    p.bound_mode = bound_mode;
+    p.quantizer = c->quantizer;
+    p.aligned16 = aligned16 ? 1 : 0;
+    const bool persistent = bound_mode != kBoundPrepass && c->pipelined_grid != 0 &&
+                            whole_blocks && aligned16 &&
+                            tiles_per_job <= c->pipelined_grid / 2;
+    if (persistent)
+        e = launch_compress_pipelined(
+            p, (uint32_t)std::min<uint64_t>(p.total_tiles, c->pipelined_grid), stream,
+            nullptr, nullptr);
+    else
+        e = launch_compress(p, stream, nullptr, nullptr);
+    if (e != hipSuccess) return hip_fail(e, "compress launch");
+    e = wait_stream(stream);
+    if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
+    if (persistent && __atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq) {
+        // Staging overflow (rates near 31 throughout): one workgroup per tile.
+        if ((rc = scratch_epoch(c, stream, &epoch))) return rc;
+        p.epoch = epoch;
+        e = launch_compress(p, stream, nullptr, nullptr);
+        if (e != hipSuccess) return hip_fail(e, "compress launch");
+        e = wait_stream(stream);
+        if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
+    }
+    rc = consume_device_error(c, stream);
+    if (rc) return rc;
+    for (size_t i = 0; i < batch; ++i) {
+        sizes_out[i] = host_sizes[i];
+        bounds_out[i] = relative ? host_bounds[i] : c->noalloc_stage[i].eps;
+    }
+    return KVSZP_OK;
 }
 
 int kvszp_compress_batch_fixed_bf16_indexed(

@@ -147,6 +147,24 @@ struct DecompressParams {
     Group groups[kMaxGroups];
 };
 
+// Device memory of the no-allocation encoder entry point
+// (kvszp_compress_batch_fixed_bf16_noalloc): one file-scope array per device
+// holding, at these byte offsets, the look-back words, the min/max words,
+// the pre-pass words and the job table of one call.
+constexpr uint32_t kNoAllocMaxJobs = 4096;
+constexpr uint32_t kNoAllocMaxTiles = 65536;   // 512 Mi values per call
+constexpr size_t kScratchTileState = 0;
+constexpr size_t kScratchTileMinMax = kScratchTileState + 8ull * kNoAllocMaxTiles;
+constexpr size_t kScratchJobMinMax = kScratchTileMinMax + 8ull * kNoAllocMaxTiles;
+constexpr size_t kScratchJobs = kScratchJobMinMax + 16ull * kNoAllocMaxJobs;
+constexpr size_t kScratchBytes = kScratchJobs + sizeof(CompressJob) * kNoAllocMaxJobs;
+
+// Device address of this device's scratch array: looked up once per device
+// (hipGetSymbolAddress with the device current) and kept.
+hipError_t scratch_address(int device, void** out);
+// Zeroes `count` 64-bit words (a fill kernel, not a memset node).
+hipError_t launch_fill_u64(unsigned long long* words, size_t count, hipStream_t stream);
+
 // Launchers (kvszp_kernels.hip).  Return hipGetLastError() of the launch.
 // Non-null events are stamped with the kernel's start / end.
 hipError_t launch_compress(const CompressParams& p, hipStream_t stream,

@@ -31,6 +31,9 @@
 
 #include <hip/hip_ext.h>
 
+#include <algorithm>
+#include <mutex>
+
 #pragma clang fp contract(off)
 
 namespace kvszp {
@@ -2406,7 +2409,51 @@ __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_
     if (err) flag_error(p.error, p.host_ctl, err);
 }
 
+__global__ void fill_u64_kernel(unsigned long long* words, size_t count) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (size_t)gridDim.x * blockDim.x)
+        words[i] = 0ull;
+}
+
 }  // namespace
+
+// ---- no-allocation scratch ---------------------------------------------------
+// The device memory of kvszp_compress_batch_fixed_bf16_noalloc (layout in
+// kvszp_internal.h).  Zero when the code object loads; every GPU holds its
+// own copy until the process ends.  Host code never uses the array's name
+// as an address: the kernels get the per-device pointer below.
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices];
+}  // namespace
+
+hipError_t scratch_address(int device, void** out) {
+    if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device] == nullptr) {
+        int current = -1;
+        hipError_t e = hipGetDevice(&current);
+        if (e != hipSuccess) return e;
+        if (current != device && (e = hipSetDevice(device)) != hipSuccess) return e;
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (current != device) (void)hipSetDevice(current);
+        if (e != hipSuccess) return e;
+        if (ptr == nullptr) return hipErrorInvalidSymbol;
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
+}
+
+hipError_t launch_fill_u64(unsigned long long* words, size_t count, hipStream_t stream) {
+    const uint32_t grid = (uint32_t)std::min<size_t>((count + 255) / 256, 1024);
+    hipLaunchKernelGGL(fill_u64_kernel, dim3(grid), dim3(256), 0, stream, words, count);
+    return hipGetLastError();
+}
 
 // Launchers.  With timing events, hipExtLaunchKernelGGL stamps them with
 // the kernel's own start and end (no separate marker packets).

@@ -48,6 +48,8 @@ EXPORTS = [
     ("kvszp_header_bytes", _sz, [_sz]),
     ("kvszp_compress_batch_fixed_bf16", _i,
      [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp]),
+    ("kvszp_compress_batch_fixed_bf16_noalloc", _i,
+     [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp]),
     ("kvszp_compress_batch_fixed_bf16_indexed", _i,
      [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _vp]),
     ("kvszp_compress_batch_fixed_bf16_indexed_groups", _i,
@@ -191,6 +193,14 @@ class Context:
     def compress(self, inputs, outputs, capacities, eps, batch, n, stream,
                  sizes_out, bounds_out) -> int:
         return self._lib.kvszp_compress_batch_fixed_bf16(
+            self.handle, inputs, outputs, capacities, eps, batch, n, stream,
+            sizes_out, bounds_out)
+
+    def compress_noalloc(self, inputs, outputs, capacities, eps, batch, n,
+                         stream, sizes_out, bounds_out) -> int:
+        """kvszp_compress_batch_fixed_bf16 without any allocation in the call
+        (device state in the library's per-GPU scratch array)."""
+        return self._lib.kvszp_compress_batch_fixed_bf16_noalloc(
             self.handle, inputs, outputs, capacities, eps, batch, n, stream,
             sizes_out, bounds_out)
 
