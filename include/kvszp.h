@@ -264,6 +264,14 @@ int kvszp_enable_timing(kvszp_ctx* ctx, int kinds);
 int kvszp_drain_timing(kvszp_ctx* ctx, double* compress_ms, int* compress_count,
                        double* decompress_ms, int* decompress_count);
 
+/* How many compress calls of this context were encoded a second time, with
+ * the schedule that needs no residency (min/max pre-pass, one workgroup per
+ * tile), because a launch's time-bounded cross-workgroup wait gave up (the
+ * device was shared with other work; KVSZP_WAIT_US sets the bound, default
+ * 200 us) or the persistent encoder's staging overflowed.  No reference
+ * counterpart: the reference's kernels assume the launch runs alone. */
+int kvszp_reencode_count(const kvszp_ctx* ctx, uint64_t* count);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* kvszp_last_error(void);
 

@@ -89,6 +89,11 @@ struct kvszp_ctx {
     int rate0 = KVSZP_RATE0_ZERO;
     uint32_t fused_tile_limit = 0;
     bool use_tickets = false;  // KVSZP_TICKETS=1: ticket-ordered tiles
+    // Time bound of the encoders' cross-workgroup waits, in steady-clock
+    // ticks (KVSZP_WAIT_US, default 200 us), and how many calls were encoded
+    // again after a launch gave up or overflowed.
+    uint64_t wait_ticks = 0;
+    uint64_t redone = 0;
     // Persistent encoder grid (co-resident workgroups); 0 = one workgroup
     // per tile (KVSZP_PERSISTENT=0, or ticket mode).
     uint32_t pipelined_grid = 0;
@@ -121,6 +126,9 @@ namespace {
 uint32_t* error_word(kvszp_ctx* c) {
     return reinterpret_cast<uint32_t*>(c->control + 1);
 }
+
+// Epoch of the last launch of this context whose bounded waits gave up.
+unsigned long long* abort_word(kvszp_ctx* c) { return c->control + 2; }
 
 int use_device(kvszp_ctx* c) {
     int cur = -1;
@@ -471,23 +479,30 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
 
     // One launch per chunk (normally one); all share the call's sequence
     // number and table, each has its own epoch (the look-back and min/max
-    // words are reused from launch to launch).
-    std::vector<CompressParams> launched(chunks.size());
-    std::vector<char> persistent(chunks.size(), 0);
-    size_t first_job = 0;
-    for (size_t k = 0; k < chunks.size(); ++k) {
+    // words are reused from launch to launch).  `safe`: the schedule that
+    // needs no residency (pre-pass bound, one workgroup per tile, untimed
+    // look-back on earlier workgroups); otherwise the fused bound and the
+    // persistent encoder where they apply, with time-bounded waits.
+    std::vector<char> redo_candidate(chunks.size(), 0);
+    std::vector<size_t> chunk_first_job(chunks.size(), 0);
+    for (size_t k = 1; k < chunks.size(); ++k) {
+        chunk_first_job[k] = chunk_first_job[k - 1];
+        for (size_t gi = chunks[k - 1].g0; gi < chunks[k - 1].g1; ++gi)
+            chunk_first_job[k] += specs[gi].jobs;
+    }
+    auto launch_chunk = [&](size_t k, bool safe) -> int {
         const Chunk& ch = chunks[k];
-        CompressParams& p = launched[k];
+        CompressParams p;
         std::memset(&p, 0, sizeof(p));
-        p.num_groups = fill_groups(p.groups, specs, ch, first_job);
-        for (size_t gi = ch.g0; gi < ch.g1; ++gi) first_job += specs[gi].jobs;
+        p.num_groups = fill_groups(p.groups, specs, ch, chunk_first_job[k]);
         int bound_mode = kBoundAbsolute;
         if (relative)
-            bound_mode = (!f32 && ch.max_tiles_per_job <= c->fused_tile_limit)
+            bound_mode = (!safe && !f32 && ch.max_tiles_per_job <= c->fused_tile_limit)
                              ? kBoundFused : kBoundPrepass;
         uint32_t epoch;
-        if ((rc = next_epoch(c, stream, &epoch))) return rc;
-        const int rec = timing_begin(c, KVSZP_KERNEL_COMPRESS);
+        int r = next_epoch(c, stream, &epoch);
+        if (r) return r;
+        const int rec = safe ? -1 : timing_begin(c, KVSZP_KERNEL_COMPRESS);
         hipError_t e;
         if (bound_mode == kBoundPrepass) {
             MinMaxParams m;
@@ -521,17 +536,21 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         p.quantizer = c->quantizer;
         p.aligned16 = aligned16 ? 1 : 0;
         p.input_f32 = f32 ? 1 : 0;
-        persistent[k] = !f32 && bound_mode != kBoundPrepass && c->pipelined_grid != 0 &&
-                        ch.whole_blocks && aligned16 &&
-                        ch.max_tiles_per_job <= c->pipelined_grid / 2;
-        if (persistent[k]) {
+        const bool persistent = !safe && !f32 && bound_mode != kBoundPrepass &&
+                                c->pipelined_grid != 0 && ch.whole_blocks && aligned16 &&
+                                ch.max_tiles_per_job <= c->pipelined_grid / 2;
+        if (persistent || bound_mode == kBoundFused) {
+            p.abort_word = abort_word(c);
+            p.wait_ticks = c->wait_ticks;
+        }
+        redo_candidate[k] = p.abort_word != nullptr;
+        if (persistent) {
             // Persistent encoder (whole, aligned, single-layer blocks only); its
             // waits are cycle-free while a job's tiles number at most the grid
-            // (half of it here, for margin).
-            CompressParams pp = p;
-            pp.ticket = nullptr;
+            // (half of it here, for margin) and all its workgroups are resident.
+            p.ticket = nullptr;
             const uint32_t grid = (uint32_t)std::min<uint64_t>(ch.tiles, c->pipelined_grid);
-            e = launch_compress_pipelined(pp, grid, stream, timing_start(c, rec),
+            e = launch_compress_pipelined(p, grid, stream, timing_start(c, rec),
                                           timing_stop(c, rec));
         } else {
             e = launch_compress(p, stream,
@@ -540,29 +559,26 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         }
         if (e != hipSuccess) return hip_fail(e, "compress launch");
         c->ticket_next += ch.tiles;
-    }
+        return KVSZP_OK;
+    };
+    for (size_t k = 0; k < chunks.size(); ++k)
+        if ((rc = launch_chunk(k, false))) return rc;
 
     // The encoder wrote sizes and bounds into pinned host memory; wait for it,
     // since callers need the sizes on the host (cuszp_wrapper.cpp:520-532).
     hipError_t e = wait_stream(stream);
     if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
-    if (__atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq) {
-        // Some wave's payload was too large for the persistent encoder's
-        // staging words (rates near 31 throughout): encode those launches
-        // again with one workgroup per tile, under fresh epochs.
-        for (size_t k = 0; k < chunks.size(); ++k) {
-            if (!persistent[k]) continue;
-            CompressParams p = launched[k];
-            uint32_t epoch;
-            if ((rc = next_epoch(c, stream, &epoch))) return rc;
-            p.epoch = epoch;
-            p.ticket_base = c->ticket_next;
-            e = launch_compress(p, stream, nullptr, nullptr);
-            if (e != hipSuccess) return hip_fail(e, "compress launch");
-            c->ticket_next += chunks[k].tiles;
-        }
+    if (__atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq ||
+        __atomic_load_n(&c->host_ctl[kHostAbort], __ATOMIC_ACQUIRE) == seq) {
+        // A persistent launch's staged payload overflowed (rates near 31
+        // throughout), or a bounded wait gave up (the device was shared):
+        // encode those launches again with the schedule that needs no
+        // residency, under fresh epochs.
+        for (size_t k = 0; k < chunks.size(); ++k)
+            if (redo_candidate[k] && (rc = launch_chunk(k, true))) return rc;
         e = wait_stream(stream);
         if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
+        c->redone += 1;
     }
     rc = consume_device_error(c, stream);
     if (rc) return rc;
@@ -726,6 +742,13 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
     {
         const char* env = std::getenv("KVSZP_TICKETS");
         c->use_tickets = env && env[0] == '1';
+        int khz = 0;
+        if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device_id) !=
+                hipSuccess || khz <= 0)
+            khz = 100000;  // the steady counter of gfx9 parts runs at 100 MHz
+        const char* us = std::getenv("KVSZP_WAIT_US");
+        const double wait_us = us ? std::atof(us) : 200.0;
+        c->wait_ticks = (uint64_t)(std::max(0.0, wait_us) * khz / 1000.0);
     }
     e = hipMalloc(&c->control, 64);
     if (e == hipSuccess) e = hipMemset(c->control, 0, 64);
@@ -964,6 +987,10 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
     const bool persistent = bound_mode != kBoundPrepass && c->pipelined_grid != 0 &&
                             whole_blocks && aligned16 &&
                             tiles_per_job <= c->pipelined_grid / 2;
+    if (persistent || bound_mode == kBoundFused) {
+        p.abort_word = words + kScratchAbort / 8;
+        p.wait_ticks = c->wait_ticks;
+    }
     if (persistent)
         e = launch_compress_pipelined(
             p, (uint32_t)std::min<uint64_t>(p.total_tiles, c->pipelined_grid), stream,
@@ -973,14 +1000,34 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
     if (e != hipSuccess) return hip_fail(e, "compress launch");
     e = wait_stream(stream);
     if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
-    if (persistent && __atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq) {
-        // Staging overflow (rates near 31 throughout): one workgroup per tile.
+    if (p.abort_word != nullptr &&
+        (__atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq ||
+         __atomic_load_n(&c->host_ctl[kHostAbort], __ATOMIC_ACQUIRE) == seq)) {
+        // Staging overflow, or a bounded wait gave up: the schedule that
+        // needs no residency (pre-pass bound, one workgroup per tile).
         if ((rc = scratch_epoch(c, stream, &epoch))) return rc;
         p.epoch = epoch;
+        p.abort_word = nullptr;
+        if (relative) {
+            p.bound_mode = kBoundPrepass;
+            MinMaxParams m;
+            std::memset(&m, 0, sizeof(m));
+            m.jobs = djobs;
+            m.job_minmax = words + kScratchJobMinMax / 8;
+            m.error = error_word(c);
+            m.host_ctl = c->host_ctl;
+            m.seq = seq;
+            m.epoch = epoch;
+            m.num_groups = 1;
+            m.groups[0] = g;
+            e = launch_minmax(m, p.total_tiles, stream, nullptr);
+            if (e != hipSuccess) return hip_fail(e, "minmax launch");
+        }
         e = launch_compress(p, stream, nullptr, nullptr);
         if (e != hipSuccess) return hip_fail(e, "compress launch");
         e = wait_stream(stream);
         if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
+        c->redone += 1;
     }
     rc = consume_device_error(c, stream);
     if (rc) return rc;
@@ -1295,6 +1342,12 @@ int kvszp_drain_timing(kvszp_ctx* c, double* compress_ms, int* compress_count,
     if (decompress_ms) *decompress_ms = ms[KVSZP_KERNEL_DECOMPRESS];
     if (decompress_count) *decompress_count = count[KVSZP_KERNEL_DECOMPRESS];
     return rc;
+}
+
+int kvszp_reencode_count(const kvszp_ctx* c, uint64_t* count) {
+    if (!c || !count) return fail(KVSZP_EINVAL, "null argument");
+    *count = c->redone;
+    return KVSZP_OK;
 }
 
 const char* kvszp_last_error(void) { return g_last_error.c_str(); }

@@ -68,6 +68,7 @@ struct Group {
 constexpr int kHostErrorMarker = 0;
 constexpr int kHostSeq = 1;
 constexpr int kHostOverflow = 2;  // seq of a persistent encode that must be redone
+constexpr int kHostAbort = 3;     // seq of an encode whose bounded waits gave up
 constexpr int kHostCtlWords = 16;
 
 struct CompressJob {
@@ -103,6 +104,13 @@ struct CompressParams {
     int quantizer;                    // 0 two roundings, 1 fused
     int aligned16;                    // every input page is 16-byte aligned
     int input_f32;                    // pages hold fp32 values (not BF16)
+    // Time-bounded waits (persistent encoder, fused bound exchange): a wait
+    // longer than wait_ticks of the steady clock stores the launch's epoch
+    // in *abort_word and seq in host_ctl[kHostAbort], and every wait of the
+    // launch then gives up; the host encodes the call again with the
+    // pre-pass schedule.  nullptr: waits bounded by kSpinLimit polls only.
+    unsigned long long* abort_word;
+    uint64_t wait_ticks;
     Group groups[kMaxGroups];
 };
 
@@ -157,7 +165,8 @@ constexpr size_t kScratchTileState = 0;
 constexpr size_t kScratchTileMinMax = kScratchTileState + 8ull * kNoAllocMaxTiles;
 constexpr size_t kScratchJobMinMax = kScratchTileMinMax + 8ull * kNoAllocMaxTiles;
 constexpr size_t kScratchJobs = kScratchJobMinMax + 16ull * kNoAllocMaxJobs;
-constexpr size_t kScratchBytes = kScratchJobs + sizeof(CompressJob) * kNoAllocMaxJobs;
+constexpr size_t kScratchAbort = kScratchJobs + sizeof(CompressJob) * kNoAllocMaxJobs;
+constexpr size_t kScratchBytes = kScratchAbort + 256;
 
 // Device address of this device's scratch array: looked up once per device
 // (hipGetSymbolAddress with the device current) and kept.

@@ -86,6 +86,45 @@ __device__ __forceinline__ void flag_error(uint32_t* e, uint32_t* host_ctl,
                        __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// Time bound of a wait of the persistent encoder or of the fused bound
+// exchange (CompressParams::abort_word).  A wait that lasts longer than
+// `ticks` of the steady clock gives up and marks the launch: the epoch goes
+// to *word and the sequence number to the host control block, and every
+// other wait of the launch gives up as soon as it reads the mark.  The host
+// then encodes the call again with the pre-pass schedule, whose only wait
+// (the look-back) is on workgroups that started earlier.  word == nullptr:
+// the wait is bounded by kSpinLimit polls and reports kErrSpin instead.
+struct WaitBound {
+    unsigned long long* word;
+    uint32_t* host_ctl;
+    uint32_t seq, epoch;
+    uint64_t ticks;
+};
+
+__device__ __forceinline__ WaitBound wait_bound(unsigned long long* word, uint32_t* host_ctl,
+                                                uint32_t seq, uint32_t epoch, uint64_t ticks) {
+    WaitBound b;
+    b.word = word;
+    b.host_ctl = host_ctl;
+    b.seq = seq;
+    b.epoch = epoch;
+    b.ticks = ticks;
+    return b;
+}
+
+// One poll of a bounded wait: true when the caller must give up.
+// `deadline` is 0 before the first poll of the wait.
+__device__ __forceinline__ bool wait_gives_up(const WaitBound& b, uint64_t& deadline) {
+    const uint64_t now = (uint64_t)wall_clock64();
+    if (deadline == 0) deadline = now + b.ticks + 1;
+    if ((uint32_t)load_relaxed(b.word) == b.epoch) return true;
+    if (now < deadline) return false;
+    store_relaxed(b.word, (unsigned long long)b.epoch);
+    __hip_atomic_store(&b.host_ctl[kHostAbort], b.seq, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+    return true;
+}
+
 // The first workgroup of a launch records the launch's sequence number in
 // the host control block: once it is visible, every copy queued on the
 // stream before this launch has completed.
@@ -518,10 +557,14 @@ __device__ __forceinline__ const unsigned long long* lookback_first_addr(
     return (tile != 0 && lane < (tile < 64u ? tile : 64u)) ? &state[t - 1 - lane] : &state[t];
 }
 
+// `bound` (optional): a time-bounded wait; when it gives up, *gave_up is
+// set, nothing is published and the result is meaningless.
 __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
                                   uint32_t tile, uint32_t total, uint32_t epoch,
                                   uint32_t* err, uint32_t* host_ctl,
-                                  bool have_first = false, unsigned long long first = 0) {
+                                  bool have_first = false, unsigned long long first = 0,
+                                  const WaitBound* bound = nullptr,
+                                  bool* gave_up = nullptr) {
     if (tile == 0) return 0;
     const int lane = __lane_id();
     const uint32_t tag_agg = epoch * 4u + 1u;
@@ -529,6 +572,8 @@ __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
     uint32_t acc = 0;
     uint32_t remaining = tile;   // earlier tiles of this job
     uint32_t pos = t - 1;        // tile read by lane 0
+    const bool timed = bound != nullptr && bound->word != nullptr;
+    uint64_t deadline = 0;
     for (;;) {
         const uint32_t nwin = remaining < 64u ? remaining : 64u;
         const bool in_win = (uint32_t)lane < nwin;
@@ -548,7 +593,12 @@ __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
                 __ballot(in_win && (tag == tag_inc || tag == tag_agg));
             need = incl ? (((incl & (~incl + 1ull)) << 1) - 1ull) : win_mask;
             if ((ready & need) == need) break;
-            if (spins >= kSpinLimit) {
+            if (timed) {
+                if (__builtin_amdgcn_readfirstlane(wait_gives_up(*bound, deadline) ? 1 : 0)) {
+                    *gave_up = true;
+                    return 0;
+                }
+            } else if (spins >= kSpinLimit) {
                 if (lane == 0) flag_error(err, host_ctl, kErrSpin);
                 need &= ready;
                 incl = 1;  // stop walking
@@ -571,9 +621,12 @@ __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
 __device__ __forceinline__ uint32_t lookback(unsigned long long* state,
                                              uint32_t t, uint32_t tile,
                                              uint32_t total, uint32_t epoch,
-                                             uint32_t* err, uint32_t* host_ctl) {
+                                             uint32_t* err, uint32_t* host_ctl,
+                                             const WaitBound* bound = nullptr,
+                                             bool* gave_up = nullptr) {
     lookback_publish(state, t, tile, total, epoch);
-    return lookback_wait(state, t, tile, total, epoch, err, host_ctl);
+    return lookback_wait(state, t, tile, total, epoch, err, host_ctl, false, 0, bound,
+                         gave_up);
 }
 
 // Finds the group of tile t (groups are few and ordered by first_tile).
@@ -751,6 +804,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     __shared__ uint32_t s_min[kThreads / 64];
     __shared__ uint32_t s_max[kThreads / 64];
     __shared__ uint32_t s_prefix;
+    __shared__ uint32_t s_abort;
     __shared__ uint8_t s_rate[kTileBlocks];
     __shared__ __attribute__((aligned(16))) uint32_t s_stage[kThreads / 64][1024];  // 4 KiB per wave
 
@@ -758,6 +812,8 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     const int lane = tid & 63;
     const int wave = tid >> 6;
     publish_seq(p.host_ctl, p.seq);
+    const WaitBound bound = wait_bound(p.abort_word, p.host_ctl, p.seq, p.epoch, p.wait_ticks);
+    if (tid == 0) s_abort = 0;
     const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {  // tickets of another launch: never index past
         if (tid == 0) flag_error(p.error, p.host_ctl, kErrSpin);
@@ -824,8 +880,14 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
             if ((uint32_t)tid < g.tiles_per_job) {
                 const unsigned long long* slot = &p.tile_minmax[t - tile + tid];
                 unsigned long long w = load_relaxed(slot);
+                uint64_t deadline = 0;
                 for (uint32_t spins = 0; (uint32_t)(w >> 32) != p.epoch; ++spins) {
-                    if (spins >= kSpinLimit) {
+                    if (bound.word != nullptr) {
+                        if (wait_gives_up(bound, deadline)) {
+                            s_abort = 1;
+                            break;
+                        }
+                    } else if (spins >= kSpinLimit) {
                         flag_error(p.error, p.host_ctl, kErrSpin);
                         break;
                     }
@@ -838,6 +900,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
             kmin = wave_min(kmin);
             kmax = wave_max(kmax);
             __syncthreads();  // s_min/s_max reuse
+            if (s_abort) return;  // the launch gave up; the host encodes again
             if (lane == 0) {
                 s_min[wave] = kmin;
                 s_max[wave] = kmax;
@@ -893,8 +956,10 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     }
 
     if (wave == 0) {
-        const uint32_t prefix =
-            lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error, p.host_ctl);
+        bool gave_up = false;
+        const uint32_t prefix = lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error,
+                                         p.host_ctl, &bound, &gave_up);
+        if (gave_up && lane == 0) s_abort = 1;
         if (lane == 0) {
             s_prefix = prefix;
             if (last_tile)
@@ -908,6 +973,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     if (bad & 1) flag_error(p.error, p.host_ctl, kErrLayerIndex);
     if (bad & 2) flag_error(p.error, p.host_ctl, kErrSpin);
     __syncthreads();
+    if (s_abort) return;
 
     // Payload (cu:302-358): sign word, then `rate` plane words.
     const uint32_t rmax = wave_max(rate);
@@ -1271,30 +1337,40 @@ constexpr float kFastLimit = 32766.0f;
 // i, i + 64, ...; all lanes end together).
 
 // `probe` (when `have_probe`) is an earlier read of lane's first word.
-__device__ __forceinline__ void job_keys(const CompressParams& p, uint32_t first_t,
+// Returns true (on every lane) when a bounded wait gave up.
+__device__ __forceinline__ bool job_keys(const CompressParams& p, uint32_t first_t,
                                          uint32_t tiles, int lane, uint32_t& kmin,
                                          uint32_t& kmax, bool have_probe,
-                                         unsigned long long probe) {
+                                         unsigned long long probe, const WaitBound& bound) {
     kmin = kKeyEmptyMin;
     kmax = kKeyEmptyMax;
+    bool gave_up = false;
     for (uint32_t i = (uint32_t)lane; i < tiles; i += 64u) {
         const unsigned long long* slot = &p.tile_minmax[first_t + i];
         unsigned long long w = have_probe && i < 64u ? probe : load_relaxed(slot);
         have_probe = false;
+        uint64_t deadline = 0;
         for (uint32_t spins = 0; (uint32_t)(w >> 32) != p.epoch; ++spins) {
-            if (spins >= kSpinLimit) {
+            if (bound.word != nullptr) {
+                if (wait_gives_up(bound, deadline)) {
+                    gave_up = true;
+                    break;
+                }
+            } else if (spins >= kSpinLimit) {
                 flag_error(p.error, p.host_ctl, kErrSpin);
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
             w = load_relaxed(slot);
         }
+        if (gave_up) break;
         const uint32_t lo = (uint32_t)(w >> 16) & 0xFFFFu, hi = (uint32_t)w & 0xFFFFu;
         kmin = lo < kmin ? lo : kmin;
         kmax = hi > kmax ? hi : kmax;
     }
     kmin = wave_min(kmin);
     kmax = wave_max(kmax);
+    return __ballot(gave_up) != 0ull;
 }
 
 // A tile's min/max keys out (one barrier): both waves reduce their lanes'
@@ -1392,6 +1468,16 @@ __device__ __forceinline__ void stage_high_words(const uint32_t* P, uint32_t cou
 // of u - G (rank u - G < t, as u < t + G/2) and look-backs of rank <=
 // u - 2G + 1/2.  Every wait depends only on waits of lower rank: no cycle
 // while all G workgroups are resident.
+//
+// Without full residency (another kernel holds CUs, or a second encoder
+// launch shares the device) a wait can depend on a workgroup that has not
+// started and cannot start while the started ones spin.  Every wait here is
+// therefore bounded in time (WaitBound): the first one to outlast the bound
+// marks the launch, every other wait gives up on reading the mark, all
+// workgroups leave at their next barrier, and the host encodes the call
+// again with the pre-pass schedule (no residency assumption).  Normal waits
+// last microseconds; the bound is hundreds, so the mark costs nothing when
+// the device is not contended.
 template <int kQuant>
 __global__ __launch_bounds__(kEncThreads)
 __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
@@ -1405,14 +1491,18 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
     __shared__ uint8_t s_rate[2][kTileBlocks];
     __shared__ PendingTile s_pend[2];  // by the parity of the tile it holds
     __shared__ uint32_t s_pwave[kEncWaves][2];  // staged: wave offset, words
+    __shared__ uint32_t s_abort;       // a bounded wait of this launch gave up
     __shared__ __attribute__((aligned(16))) uint32_t s_stage[kEncWaves][kEncStageWords];
 
     publish_seq(p.host_ctl, p.seq);
     if ((int)threadIdx.x < p.num_groups) s_gfirst[threadIdx.x] = p.groups[threadIdx.x].first_tile;
+    if (threadIdx.x == 0) s_abort = 0;
     __syncthreads();
     const uint32_t G = gridDim.x;
     const bool fused = p.bound_mode == kBoundFused;
+    const WaitBound bound = wait_bound(p.abort_word, p.host_ctl, p.seq, p.epoch, p.wait_ticks);
     bool pending = false;  // a tile's payload waits in the staging words
+    bool aborted = false;  // stop: the host encodes this launch again
 
     // Prologue: the first tile and its keys (published).
     TileCtx cur = tile_ctx(p, blockIdx.x, s_gfirst);
@@ -1512,7 +1602,9 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
             uint32_t fast = 0;
             if (fused) {
                 uint32_t kmin, kmax;
-                job_keys(p, cur.t - cur.tile, g.tiles_per_job, lane, kmin, kmax, true, probe);
+                if (job_keys(p, cur.t - cur.tile, g.tiles_per_job, lane, kmin, kmax, true, probe,
+                             bound) && lane == 0)
+                    s_abort = 1;
                 eb = relative_bound(eps, kmin, kmax);
                 const float jabs = fmaxf(fabsf(min_key_value(kmin)), fabsf(max_key_value(kmax)));
                 fast = jabs * (0.5f / eb) <= kFastLimit ? 1u : 0u;
@@ -1524,6 +1616,10 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
             }
         }
         __syncthreads();
+        if (s_abort) {
+            aborted = true;
+            return false;
+        }
         if (has_next) {
             if (fused && tid == 0) {
                 const uint32_t kmin = min(s_min[0], s_min[1]), kmax = max(s_max[0], s_max[1]);
@@ -1608,8 +1704,11 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         // in the previous iteration); one barrier hands the prefix over.
         if (wave == 1 && pending) {
             const PendingTile& q = s_pend[parity ^ 1u];
+            bool gave_up = false;
             const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                              p.epoch, p.error, p.host_ctl, true, probe);
+                                              p.epoch, p.error, p.host_ctl, true, probe,
+                                              &bound, &gave_up);
+            if (gave_up && lane == 0) s_abort = 1;
             if (lane == 0) {
                 s_prefix[parity] = pf;
                 if (q.last)
@@ -1621,6 +1720,10 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
             }
         }
         __syncthreads();
+        if (s_abort) {
+            aborted = true;
+            return false;
+        }
 
         // d. the pending tile's payload out (frees the staging words)
         if (pending) {
@@ -1712,14 +1815,17 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         parity ^= 1u;
     }
     // The last staged payload.
-    if (pending) {
+    if (pending && !aborted) {
         const int tid = loop_tid();
         const int lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         if (wave == 1) {
             const PendingTile& q = s_pend[parity];
+            bool gave_up = false;
             const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                              p.epoch, p.error, p.host_ctl);
+                                              p.epoch, p.error, p.host_ctl, false, 0,
+                                              &bound, &gave_up);
+            if (gave_up && lane == 0) s_abort = 1;
             if (lane == 0) {
                 s_prefix[2] = pf;
                 if (q.last)
@@ -1731,6 +1837,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
             }
         }
         __syncthreads();
+        if (s_abort) return;
         const PendingTile& q = s_pend[parity];
         const uint32_t woff = s_pwave[wave][0], words = s_pwave[wave][1];
         if (words)

@@ -74,6 +74,7 @@ EXPORTS = [
     ("kvszp_synchronize", _i, [_vp, _vp]),
     ("kvszp_enable_timing", _i, [_vp, _i]),
     ("kvszp_drain_timing", _i, [_vp, _vp, _vp, _vp, _vp]),
+    ("kvszp_reencode_count", _i, [_vp, _vp]),
     ("kvszp_last_error", ctypes.c_char_p, []),
 ]
 
@@ -280,6 +281,13 @@ class Context:
         return self._lib.kvszp_decompress_batch_fixed_f32(
             self.handle, compressed, sizes, bounds, batch, outputs, numels,
             stream)
+
+    def reencode_count(self) -> int:
+        """Compress calls encoded again with the pre-pass schedule (a
+        bounded wait gave up, or the persistent staging overflowed)."""
+        n = ctypes.c_uint64()
+        check(self._lib.kvszp_reencode_count(self.handle, ctypes.byref(n)))
+        return n.value
 
     def synchronize(self, stream) -> int:
         return self._lib.kvszp_synchronize(self.handle, stream)

@@ -1,0 +1,203 @@
+"""The encoder on a shared device: results stay byte-exact and every call
+ends when its launch cannot have all its workgroups resident.
+
+The persistent encoder and the fused bound exchange wait on other
+workgroups of the same launch; with another kernel holding CUs, or a second
+encoder launch on another stream, some of those workgroups may not start
+while the started ones wait.  Those waits are bounded in time; when one
+gives up, the launch stops and the call is encoded again with the pre-pass
+schedule (kvszp_reencode_count counts such calls).  The connector runs its
+stores on a worker thread beside vLLM's model kernels
+(vllm_v1_compressed_offload.py:2365-2385), so these are the conditions it
+meets.  Workload: the full benchmark configuration 1 (256 Qwen2.5-1.5B pages,
+21 layers at REL 1e-4 and 7 at 1e-5, 512 segment requests in one grouped
+call), every stream checked against the oracle.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def c1(oracle):
+    """Config 1 pages on the device and the oracle's streams of every
+    segment request (group by group, page by page)."""
+    import kv_synth
+
+    shape = kv_synth.QWEN25_1P5B_4K
+    pages = kv_synth.paged_kv(shape, seed=0, device=DEV)
+    host = pages.view(torch.int16).cpu().numpy().view(np.uint16)
+    groups = kv_synth.mixed_bound_groups()
+    want = []
+    for bound, layers in groups:
+        streams, sizes, bounds = oracle.compress_batch(
+            host, [bound] * host.shape[0], relative=True, threads=8,
+            layer_indices=list(layers), source_layers=shape.layers,
+            elements_per_layer=shape.elements_per_layer)
+        want += list(zip(streams, bounds))
+    return dict(shape=shape, pages=pages, groups=groups, want=want)
+
+
+def _requests(c1):
+    shape, pages = c1["shape"], c1["pages"]
+    inputs, caps, eps, idx, counts = [], [], [], [], []
+    for bound, layers in c1["groups"]:
+        n = 2 * len(layers) * shape.elements_per_layer
+        idx.append(torch.tensor(layers, dtype=torch.long, device=DEV))
+        counts.append(pages.shape[0])
+        for p in range(pages.shape[0]):
+            inputs.append(pages[p])
+            caps.append(8 * n)
+            eps.append(bound)
+    slab = torch.empty(sum(caps), dtype=torch.uint8, device=DEV)
+    bufs, off = [], 0
+    for cap in caps:
+        bufs.append(slab[off:off + cap])
+        off += cap
+    return inputs, bufs, eps, idx, counts
+
+
+def _wrapper():
+    import cuszp_wrapper_cpp as cpp
+
+    cfg = cpp.CompressionConfig(1e-4, True, cpp.DIM_1D, cpp.MODE_FIXED, cpp.TYPE_FLOAT)
+    return cpp.CuSZpWrapper(cfg, 0)
+
+
+def _compress(w, c1, req):
+    inputs, bufs, eps, idx, counts = req
+    shape = c1["shape"]
+    return w.compress_batch_fixed_bf16_indexed_groups(
+        inputs, bufs, idx, counts, 2, shape.layers, shape.elements_per_layer, eps)
+
+
+def _check(c1, bufs, sizes, bounds):
+    assert len(sizes) == len(c1["want"])
+    host = [b.cpu().numpy() for b in bufs]  # one copy per request slice
+    for k, (stream, eb) in enumerate(c1["want"]):
+        assert np.float32(bounds[k]) == np.float32(eb), k
+        assert sizes[k] == stream.size, k
+        assert np.array_equal(host[k][:sizes[k]], stream), k
+
+
+def test_full_size_config1_store_and_restore_match_oracle(c1, oracle):
+    """All 512 segment streams of the benchmark step, then the grouped
+    restore of all 256 pages, byte for byte against the oracle."""
+    w = _wrapper()
+    req = _requests(c1)
+    ok, sizes, bounds = _compress(w, c1, req)
+    assert ok
+    _check(c1, req[1], sizes, bounds)
+    shape, pages = c1["shape"], c1["pages"]
+    dest = torch.zeros_like(pages)
+    _, bufs, _, idx, counts = req
+    assert w.decompress_batch_fixed_bf16_indexed_scatter_groups(
+        bufs, sizes, [dest[p] for p in range(pages.shape[0])] * len(counts), idx,
+        counts, 2, shape.layers, shape.elements_per_layer, bounds)
+    assert w.synchronize()
+    want = np.zeros((pages.shape[0], pages.shape[1]), dtype=np.uint16)
+    k = 0
+    for bound, layers in c1["groups"]:
+        n = 2 * len(layers) * shape.elements_per_layer
+        for p in range(pages.shape[0]):
+            stream, eb = c1["want"][k]
+            oracle.decompress_indexed(stream, n, float(eb), want[p], list(layers),
+                                      shape.layers, shape.elements_per_layer)
+            k += 1
+    got = dest.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_forced_give_up_encodes_again_exactly(c1, monkeypatch):
+    """A wait bound of zero makes the first wait that is not met at once
+    give up: the call is encoded again with the pre-pass schedule and must
+    produce the same bytes."""
+    monkeypatch.setenv("KVSZP_WAIT_US", "0")
+    w = _wrapper()
+    req = _requests(c1)
+    for _ in range(3):
+        ok, sizes, bounds = _compress(w, c1, req)
+        assert ok
+        _check(c1, req[1], sizes, bounds)
+    assert w._ctx.reencode_count() > 0
+    # the fused bound exchange of the one-workgroup-per-tile kernel (blocks
+    # not whole: n % 32 != 0) gives up and is encoded again too
+    n = 8192 * 5 + 7
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(6, n, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    bufs = [torch.empty(8 * n + 2048, dtype=torch.uint8, device=DEV) for _ in range(6)]
+    before = w._ctx.reencode_count()
+    ok, sizes, bounds = w.compress_batch_fixed_bf16(list(x), bufs, [1e-4] * 6)
+    assert ok
+    import oracle
+
+    bits = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    for i in range(6):
+        eb = oracle.relative_bound(bits[i], n, 1e-4)
+        assert np.float32(bounds[i]) == np.float32(eb)
+        want = oracle.compress_page(bits[i], n, float(eb))
+        assert np.array_equal(bufs[i][:sizes[i]].cpu().numpy(), want), i
+    assert w._ctx.reencode_count() >= before
+
+
+def test_two_encoders_on_two_streams(c1):
+    """Two contexts encode the full configuration at the same time from two
+    host threads on two streams, each persistent launch sized for the whole
+    device."""
+    results, errors = {}, []
+
+    def worker(name):
+        try:
+            w = _wrapper()
+            req = _requests(c1)
+            stream = torch.cuda.Stream()
+            out = []
+            with torch.cuda.stream(stream):
+                for _ in range(4):
+                    ok, sizes, bounds = _compress(w, c1, req)
+                    assert ok
+                    out.append(([b.clone() for b in req[1]], sizes, bounds))
+            torch.cuda.synchronize()
+            results[name] = out
+        except Exception as exc:  # reported below
+            errors.append(repr(exc))
+
+    threads = [threading.Thread(target=worker, args=(n,)) for n in ("a", "b")]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "an encoder call did not return"
+    assert not errors, errors
+    for name in ("a", "b"):
+        for bufs, sizes, bounds in results[name]:
+            _check(c1, bufs, sizes, bounds)
+
+
+def test_encoder_beside_a_busy_kernel(c1):
+    """Matrix products on a second stream hold the CUs while the store runs
+    on the current stream (the connector's store thread beside the model)."""
+    a = torch.randn(8192, 8192, dtype=torch.bfloat16, device=DEV)
+    b = torch.randn(8192, 8192, dtype=torch.bfloat16, device=DEV)
+    busy = torch.cuda.Stream()
+    w = _wrapper()
+    req = _requests(c1)
+    for _ in range(3):
+        torch.cuda.synchronize()
+        with torch.cuda.stream(busy):
+            for _ in range(20):
+                c = torch.mm(a, b)
+        ok, sizes, bounds = _compress(w, c1, req)
+        assert ok
+        _check(c1, req[1], sizes, bounds)
+    torch.cuda.synchronize()
+    assert torch.isfinite(c[:4, :4].float()).all()
