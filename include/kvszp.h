@@ -239,6 +239,37 @@ int kvszp_decompress_batch_fixed_f32(kvszp_ctx* ctx,
                                      const uint64_t* num_elements,
                                      kvszp_stream_t stream);
 
+/* ---- packed publication and restore --------------------------------------- */
+
+/* Replaces CompressedPageStore.put_many_packed
+ * (vllm_v1_compressed_offload.py:371-447): payload i (any device buffer,
+ * sizes[i] bytes, e.g. a stream written by a compress call or a raw page) is
+ * placed at offsets_out[i] of `slab`, the offsets being the 8-byte-aligned
+ * exclusive scan of the sizes (gaps zeroed); *packed_bytes_out = end of the
+ * last payload.  `slab` is normally pinned host memory (hipHostMalloc, torch
+ * pin_memory): one gather kernel then writes every payload across the link,
+ * which is the device-to-host transfer (the reference concatenates on the
+ * device with torch.cat and copies the result).  Device memory works too.
+ * Blocks until the slab is complete, like the reference (:429-430). */
+int kvszp_pack_streams(kvszp_ctx* ctx, const void* const* payloads,
+                       const uint64_t* sizes, size_t count, void* slab,
+                       uint64_t slab_capacity, kvszp_stream_t stream,
+                       uint64_t* offsets_out, uint64_t* packed_bytes_out);
+
+/* The packed restore of a grouped indexed store
+ * (vllm_v1_compressed_offload.py:1618-1711 then :1815-2006): one
+ * host-to-device copy of `packed_bytes` from the pinned slab `packed` into
+ * the device buffer `staging`, then
+ * kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups with stream i at
+ * staging + offsets[i].  Enqueue only. */
+int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
+    kvszp_ctx* ctx, const void* packed, uint64_t packed_bytes, void* staging,
+    uint64_t staging_capacity, const uint64_t* offsets, const uint64_t* sizes,
+    const float* error_bounds, size_t batch, void* const* destinations,
+    const int64_t* const* layer_indices, const size_t* selected_layers,
+    const size_t* group_sizes, size_t num_groups, size_t prefix_count,
+    size_t source_layers, size_t elements_per_layer, kvszp_stream_t stream);
+
 /* Waits for `stream` and reports any error a kernel of this context flagged
  * since the last check (decompress calls only enqueue, so their device-side
  * errors surface here or at the next compress call).  No reference

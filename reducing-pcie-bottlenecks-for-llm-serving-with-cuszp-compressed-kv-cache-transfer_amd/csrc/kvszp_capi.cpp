@@ -1301,6 +1301,89 @@ int kvszp_decompress_batch_fixed_f32(kvszp_ctx* c, const void* const* compressed
                           num_elements, (hipStream_t)stream);
 }
 
+int kvszp_pack_streams(kvszp_ctx* c, const void* const* payloads, const uint64_t* sizes,
+                       size_t count, void* slab, uint64_t slab_capacity,
+                       kvszp_stream_t stream_handle, uint64_t* offsets_out,
+                       uint64_t* packed_bytes_out) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    hipStream_t stream = (hipStream_t)stream_handle;
+    if (count == 0) return fail(KVSZP_EINVAL, "nothing to pack");
+    if (!payloads || !sizes || !slab || !offsets_out || !packed_bytes_out)
+        return fail(KVSZP_EINVAL, "null pointer argument");
+    int rc = use_device(c);
+    if (rc) return rc;
+    // vllm_v1_compressed_offload.py:385-392: start = align8(end of the
+    // previous payload); the slab ends with the last payload.
+    std::vector<PackJob> jobs(count);
+    uint64_t end = 0;
+    for (size_t i = 0; i < count; ++i) {
+        if (sizes[i] && !payloads[i]) return fail(KVSZP_EINVAL, "null payload %zu", i);
+        const uint64_t start = (end + 7) & ~7ull;
+        if (i > 0) jobs[i - 1].pad = start - end;
+        jobs[i].src = static_cast<const uint8_t*>(payloads[i]);
+        jobs[i].dst_off = start;
+        jobs[i].size = sizes[i];
+        jobs[i].pad = 0;
+        offsets_out[i] = start;
+        end = start + sizes[i];
+    }
+    if (end > slab_capacity)
+        return fail(KVSZP_EINVAL, "slab holds %llu bytes, the packed payloads %llu",
+                    (unsigned long long)slab_capacity, (unsigned long long)end);
+    *packed_bytes_out = end;
+    const uint32_t seq = ++c->seq;
+    if ((rc = upload_tables(c, jobs.data(), count * sizeof(PackJob), seq, stream))) return rc;
+    PackParams p;
+    p.jobs = reinterpret_cast<const PackJob*>(c->tables.ptr);
+    p.dst = static_cast<uint8_t*>(slab);
+    p.count = (uint32_t)count;
+    p.host_ctl = c->host_ctl;
+    p.seq = seq;
+    // Writes into pinned host memory run at the link's rate from a few dozen
+    // workgroups; more only take CUs from other work.
+    const uint32_t grid = (uint32_t)std::min<size_t>(count, 128);
+    hipError_t e = launch_pack(p, grid, stream);
+    if (e != hipSuccess) return hip_fail(e, "pack launch");
+    // The slab is complete when the call returns (the reference synchronizes
+    // after its device-to-host copy, :429-430).
+    e = wait_stream(stream);
+    if (e != hipSuccess) return hip_fail(e, "waiting for the pack");
+    return KVSZP_OK;
+}
+
+int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
+    kvszp_ctx* c, const void* packed, uint64_t packed_bytes, void* staging,
+    uint64_t staging_capacity, const uint64_t* offsets, const uint64_t* sizes,
+    const float* error_bounds, size_t batch, void* const* destinations,
+    const int64_t* const* layer_indices, const size_t* selected_layers,
+    const size_t* group_sizes, size_t num_groups, size_t prefix_count,
+    size_t source_layers, size_t elements_per_layer, kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (batch == 0) return KVSZP_OK;
+    if (!packed || !staging || !offsets || !sizes)
+        return fail(KVSZP_EINVAL, "null pointer argument");
+    if (packed_bytes > staging_capacity)
+        return fail(KVSZP_EINVAL, "staging holds %llu bytes, the slab %llu",
+                    (unsigned long long)staging_capacity, (unsigned long long)packed_bytes);
+    std::vector<const void*> streams(batch);
+    for (size_t i = 0; i < batch; ++i) {
+        if (offsets[i] > packed_bytes || sizes[i] > packed_bytes - offsets[i])
+            return fail(KVSZP_EINVAL, "payload %zu lies outside the slab", i);
+        streams[i] = static_cast<const uint8_t*>(staging) + offsets[i];
+    }
+    int rc = use_device(c);
+    if (rc) return rc;
+    // vllm_v1_compressed_offload.py:1648-1676: one host-to-device copy of the
+    // packed slab, then decode from it.
+    hipError_t e = hipMemcpyAsync(staging, packed, packed_bytes, hipMemcpyHostToDevice,
+                                  (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D packed slab)");
+    return kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups(
+        c, streams.data(), sizes, error_bounds, batch, destinations, layer_indices,
+        selected_layers, group_sizes, num_groups, prefix_count, source_layers,
+        elements_per_layer, stream);
+}
+
 int kvszp_synchronize(kvszp_ctx* c, kvszp_stream_t stream) {
     if (!c) return fail(KVSZP_EINVAL, "null context");
     int rc = use_device(c);

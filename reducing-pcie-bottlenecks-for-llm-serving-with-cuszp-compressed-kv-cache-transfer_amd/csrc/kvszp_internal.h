@@ -155,6 +155,26 @@ struct DecompressParams {
     Group groups[kMaxGroups];
 };
 
+// Packed publication: every payload i (src, size bytes) goes to
+// dst + dst_off, dst_off an 8-byte-aligned exclusive scan of the sizes; the
+// gap up to the next payload is zeroed.  dst may be pinned host memory.
+struct PackJob {
+    const uint8_t* src;
+    uint64_t dst_off;
+    uint64_t size;
+    uint64_t pad;                     // zero bytes written after the payload
+};
+
+struct PackParams {
+    const PackJob* jobs;
+    uint8_t* dst;
+    uint32_t count;
+    uint32_t* host_ctl;
+    uint32_t seq;
+};
+
+hipError_t launch_pack(const PackParams& p, uint32_t grid, hipStream_t stream);
+
 // Device memory of the no-allocation encoder entry point
 // (kvszp_compress_batch_fixed_bf16_noalloc): one file-scope array per device
 // holding, at these byte offsets, the look-back words, the min/max words,

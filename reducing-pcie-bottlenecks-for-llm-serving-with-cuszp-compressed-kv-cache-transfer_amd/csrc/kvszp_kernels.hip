@@ -2516,6 +2516,43 @@ __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_
     if (err) flag_error(p.error, p.host_ctl, err);
 }
 
+// ---- packed publication ------------------------------------------------------
+// Workgroup b copies payloads b, b + G, ... to their packed offsets: 8-byte
+// lanes when source and destination allow it (a wave moves 512 contiguous
+// bytes per instruction), else 4-byte or single-byte lanes, then zeroes the
+// alignment gap behind the payload.  The destination is normally pinned host
+// memory, so the copy is the device-to-host transfer itself.
+__global__ __launch_bounds__(256) void pack_kernel(PackParams p) {
+    publish_seq(p.host_ctl, p.seq);
+    for (uint32_t j = blockIdx.x; j < p.count; j += gridDim.x) {
+        const PackJob J = load_const(p.jobs, j);
+        const uint8_t* src = J.src;
+        uint8_t* dst = p.dst + J.dst_off;
+        const uint64_t n = J.size;
+        const uintptr_t mis = (uintptr_t)src | (uintptr_t)dst;
+        uint64_t done = 0;
+        if ((mis & 7u) == 0) {
+            typedef __attribute__((address_space(1))) unsigned long long g_u64;
+            const g_u64* s8 = (const g_u64*)src;
+            g_u64* d8 = (g_u64*)dst;
+            const uint64_t words = n >> 3;
+            for (uint64_t i = threadIdx.x; i < words; i += blockDim.x) d8[i] = s8[i];
+            done = words << 3;
+        } else if ((mis & 3u) == 0) {
+            const g_u32* s4 = (const g_u32*)src;
+            g_u32* d4 = (g_u32*)dst;
+            const uint64_t words = n >> 2;
+            for (uint64_t i = threadIdx.x; i < words; i += blockDim.x) d4[i] = s4[i];
+            done = words << 2;
+        }
+        typedef __attribute__((address_space(1))) uint8_t g_u8;
+        const g_u8* s1 = (const g_u8*)src;
+        g_u8* d1 = (g_u8*)dst;
+        for (uint64_t i = done + threadIdx.x; i < n; i += blockDim.x) d1[i] = s1[i];
+        if (threadIdx.x < J.pad) d1[n + threadIdx.x] = 0;
+    }
+}
+
 __global__ void fill_u64_kernel(unsigned long long* words, size_t count) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
          i += (size_t)gridDim.x * blockDim.x)
@@ -2554,6 +2591,11 @@ hipError_t scratch_address(int device, void** out) {
     }
     *out = g_scratch_ptr[device];
     return hipSuccess;
+}
+
+hipError_t launch_pack(const PackParams& p, uint32_t grid, hipStream_t stream) {
+    hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(256), 0, stream, p);
+    return hipGetLastError();
 }
 
 hipError_t launch_fill_u64(unsigned long long* words, size_t count, hipStream_t stream) {

@@ -494,6 +494,78 @@ class CuSZpWrapper:
             return False
         return True
 
+    # ---- packed publication and restore (no pybind counterpart) ----------
+
+    def pack_payloads(self, payloads, slab):
+        """The device half of CompressedPageStore.put_many_packed
+        (vllm_v1_compressed_offload.py:371-447): every payload (a uint8 device
+        tensor: a stream slice or a raw page's bytes) goes to `slab` at the
+        8-byte-aligned exclusive scan of the sizes, gaps zeroed.  `slab` is
+        normally a pinned host uint8 tensor: one gather kernel then writes the
+        payloads across the link (the device-to-host copy itself).  Blocks
+        until the slab is complete.  Returns (ok, offsets, packed_bytes)."""
+        count = len(payloads)
+        if count == 0 or slab.dtype != torch.uint8 or not slab.is_contiguous():
+            return (False, [], 0)
+        if not (slab.is_pinned() or self._on_device(slab)):
+            return (False, [], 0)
+        for t in payloads:
+            if not self._on_device(t) or not t.is_contiguous():
+                return (False, [], 0)
+        offsets = (ctypes.c_uint64 * count)()
+        total = ctypes.c_uint64()
+        rc = self._ctx.pack(
+            kvszp.ptr_array([t.data_ptr() for t in payloads]),
+            kvszp.u64_array([t.numel() * t.element_size() for t in payloads]),
+            count, slab.data_ptr(), slab.numel(), _stream_handle(self._device_id),
+            offsets, ctypes.byref(total))
+        if rc != kvszp.OK:
+            _report("packing payloads failed")
+            return (False, [], 0)
+        return (True, [int(o) for o in offsets], int(total.value))
+
+    def decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
+            self, packed, packed_bytes, staging, offsets, compressed_sizes,
+            output_tensors, layer_indices, group_sizes, prefix_count,
+            source_layers, elements_per_layer, actual_error_bounds):
+        """The packed restore (vllm_v1_compressed_offload.py:1618-1711): one
+        host-to-device copy of the pinned slab `packed` into the uint8 device
+        tensor `staging`, then the grouped indexed scatter of the streams at
+        `offsets`.  Enqueue only."""
+        batch = len(offsets)
+        if batch == 0:
+            return True
+        if (len(compressed_sizes) != batch or len(actual_error_bounds) != batch
+                or len(output_tensors) != batch or not layer_indices
+                or len(layer_indices) != len(group_sizes)
+                or not self._fixed_mode() or not packed.is_pinned()
+                or not self._on_device(staging) or staging.dtype != torch.uint8
+                or sum(int(g) for g in group_sizes) != batch):
+            return False
+        for idx in layer_indices:
+            if not self._layer_index_ok(idx, source_layers):
+                return False
+        source_elements = prefix_count * source_layers * elements_per_layer
+        for out in output_tensors:
+            if (not self._on_device(out) or out.dtype != torch.bfloat16
+                    or not out.is_contiguous() or out.numel() < source_elements):
+                return False
+        rc = self._ctx.decompress_indexed_scatter_groups_packed(
+            packed.data_ptr(), int(packed_bytes), staging.data_ptr(),
+            staging.numel(), kvszp.u64_array([int(o) for o in offsets]),
+            kvszp.u64_array([int(s) for s in compressed_sizes]),
+            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
+            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
+            kvszp.ptr_array([t.data_ptr() for t in layer_indices]),
+            kvszp.size_array([t.numel() for t in layer_indices]),
+            kvszp.size_array([int(g) for g in group_sizes]), len(group_sizes),
+            prefix_count, source_layers, elements_per_layer,
+            _stream_handle(self._device_id))
+        if rc != kvszp.OK:
+            _report("packed grouped indexed scatter decompression failed")
+            return False
+        return True
+
     def synchronize(self) -> bool:
         """Waits for the current stream and reports device-side errors of
         earlier (enqueue-only) decompress calls.  No reference counterpart."""

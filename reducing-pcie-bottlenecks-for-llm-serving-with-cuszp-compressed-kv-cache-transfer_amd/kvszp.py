@@ -71,6 +71,11 @@ EXPORTS = [
      [_vp, _vp, ctypes.c_uint64, _vp, _sz, ctypes.c_float, _vp]),
     ("kvszp_decompress_batch_fixed_f32", _i,
      [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
+    ("kvszp_pack_streams", _i,
+     [_vp, _vp, _vp, _sz, _vp, ctypes.c_uint64, _vp, _vp, _vp]),
+    ("kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups_packed", _i,
+     [_vp, _vp, ctypes.c_uint64, _vp, ctypes.c_uint64, _vp, _vp, _vp, _sz, _vp,
+      _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
     ("kvszp_synchronize", _i, [_vp, _vp]),
     ("kvszp_enable_timing", _i, [_vp, _i]),
     ("kvszp_drain_timing", _i, [_vp, _vp, _vp, _vp, _vp]),
@@ -281,6 +286,23 @@ class Context:
         return self._lib.kvszp_decompress_batch_fixed_f32(
             self.handle, compressed, sizes, bounds, batch, outputs, numels,
             stream)
+
+    def pack(self, payloads, sizes, count, slab, slab_capacity, stream,
+             offsets_out, packed_bytes_out) -> int:
+        return self._lib.kvszp_pack_streams(
+            self.handle, payloads, sizes, count, slab, slab_capacity, stream,
+            offsets_out, packed_bytes_out)
+
+    def decompress_indexed_scatter_groups_packed(
+            self, packed, packed_bytes, staging, staging_capacity, offsets,
+            sizes, bounds, batch, destinations, layer_indices, selected_layers,
+            group_sizes, num_groups, prefix_count, source_layers,
+            elements_per_layer, stream) -> int:
+        return self._lib.kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
+            self.handle, packed, packed_bytes, staging, staging_capacity,
+            offsets, sizes, bounds, batch, destinations, layer_indices,
+            selected_layers, group_sizes, num_groups, prefix_count,
+            source_layers, elements_per_layer, stream)
 
     def reencode_count(self) -> int:
         """Compress calls encoded again with the pre-pass schedule (a

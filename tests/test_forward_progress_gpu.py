@@ -27,57 +27,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.fixture(scope="module")
-def c1(oracle):
-    """Config 1 pages on the device and the oracle's streams of every
-    segment request (group by group, page by page)."""
-    import kv_synth
-
-    shape = kv_synth.QWEN25_1P5B_4K
-    pages = kv_synth.paged_kv(shape, seed=0, device=DEV)
-    host = pages.view(torch.int16).cpu().numpy().view(np.uint16)
-    groups = kv_synth.mixed_bound_groups()
-    want = []
-    for bound, layers in groups:
-        streams, sizes, bounds = oracle.compress_batch(
-            host, [bound] * host.shape[0], relative=True, threads=8,
-            layer_indices=list(layers), source_layers=shape.layers,
-            elements_per_layer=shape.elements_per_layer)
-        want += list(zip(streams, bounds))
-    return dict(shape=shape, pages=pages, groups=groups, want=want)
-
-
-def _requests(c1):
-    shape, pages = c1["shape"], c1["pages"]
-    inputs, caps, eps, idx, counts = [], [], [], [], []
-    for bound, layers in c1["groups"]:
-        n = 2 * len(layers) * shape.elements_per_layer
-        idx.append(torch.tensor(layers, dtype=torch.long, device=DEV))
-        counts.append(pages.shape[0])
-        for p in range(pages.shape[0]):
-            inputs.append(pages[p])
-            caps.append(8 * n)
-            eps.append(bound)
-    slab = torch.empty(sum(caps), dtype=torch.uint8, device=DEV)
-    bufs, off = [], 0
-    for cap in caps:
-        bufs.append(slab[off:off + cap])
-        off += cap
-    return inputs, bufs, eps, idx, counts
-
-
-def _wrapper():
-    import cuszp_wrapper_cpp as cpp
-
-    cfg = cpp.CompressionConfig(1e-4, True, cpp.DIM_1D, cpp.MODE_FIXED, cpp.TYPE_FLOAT)
-    return cpp.CuSZpWrapper(cfg, 0)
-
-
-def _compress(w, c1, req):
-    inputs, bufs, eps, idx, counts = req
-    shape = c1["shape"]
-    return w.compress_batch_fixed_bf16_indexed_groups(
-        inputs, bufs, idx, counts, 2, shape.layers, shape.elements_per_layer, eps)
+from conftest import c1_compress as _compress, c1_requests as _requests, fixed_wrapper as _wrapper
 
 
 def _check(c1, bufs, sizes, bounds):
