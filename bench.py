@@ -1,34 +1,64 @@
 #!/usr/bin/env python3
 """Benchmark: batched fixed-mode BF16 KV-page store + restore on one MI355X.
 
-Workload: the full Qwen2.5-1.5B 4K-context KV
-cache, 28 layers x K/V x [4096 tokens, 2 heads, 128] BF16, laid out as 256
-vLLM pages of [2, 28, 16, 2, 128] (229 376 values, 448 KiB each).  Layer
-bounds follow the reference's measured mixed profile: layers
-{0,1,2,5,19,20,21} at REL 1e-5, the other 21 at REL 1e-4, so every page is
-two layer-selected segments.  One step is what the reference's connector
-does for this job (vllm_v1_compressed_offload.py:1286-1569 and 1815-2006):
+Metric: KV compress/decompress GB/s of BF16 input, % of HBM
+peak, compression ratio.  One step is what the reference's connector does
+for one transfer job (vllm_v1_compressed_offload.py:825-1028 / 1286-1569 for
+the store, :1815-2006 for the restore), through the C ABI (libkvszp.so) with
+every pointer table built once and the pages resident in HBM:
 
-  store   : one compress_batch_fixed_bf16_indexed_groups call over all 512
-            (page, segment) requests (blocking: sizes come back to the host)
-  restore : the reference's one decompress_batch_fixed_bf16_indexed_scatter
-            call per group, writing straight into fresh KV pages -- by
-            default as ONE decompress_batch_fixed_bf16_indexed_scatter_groups
-            launch over both groups (same output; --restore-per-group runs
-            the per-group calls instead)
+  --config 1 (default; the metric's configuration): the full Qwen2.5-1.5B
+      4K-context KV cache, 256 vLLM pages of [2, 28, 16, 2, 128] BF16, layers
+      {0,1,2,5,19,20,21} at REL 1e-5 and the other 21 at 1e-4:
+      store   = one compress_batch_fixed_bf16_indexed_groups call over all
+                512 (page, layer group) requests (blocking: sizes come back)
+      restore = one decompress_batch_fixed_bf16_indexed_scatter_groups launch
+                into fresh pages (--restore-per-group: the reference's one
+                indexed_scatter call per group)
+  --config 0: one layer's K and V (2 pages of 1 048 576), REL 1e-4, uniform
+      store + contiguous restore
+  --config 2: 8192 pages of a 16 x 8192-token pool in page-table order,
+      REL 1e-4, uniform store + restore into permuted fresh slots
+  --config 3: Qwen2.5-7B 32K (2048 pages of 458 752, RoPE-like K), REL 1e-5,
+      uniform store + restore into permuted fresh slots
+  --config 4: Llama-3-8B 64K stress pages (4096 pages of 1 048 576: zero,
+      constant, heavy-tailed, Gaussian), per-layer REL 1e-4/1e-5 alternating:
+      grouped indexed store + grouped restore
 
-Calls go through the C ABI (libkvszp.so) with the page-pointer arrays built
-once, inputs resident in HBM.  `value` = uncompressed BF16 bytes of the KV
-cache / (store + restore time per step).  Kernel-only throughput and the
-roofline fraction come from HIP events recorded on the launch stream.
+Reported (one JSON line):
+  value            BF16 bytes of the job / wall time per step (store+restore)
+                   over K timed steps.  Each step uses the next of --rotate
+                   buffer sets (pages, streams, destinations), so that a step
+                   re-reads nothing the 256 MB Infinity Cache still holds from
+                   the step before (default 3 sets for configs 0 and 1, whose
+                   working set is below 256 MB; the other configs exceed it).
+                   value_mall_warm: the same steps on one buffer set.
+  kernel times     per-launch durations from HIP events recorded by the
+                   library on the launch stream: mean, min, median.
+  roofline         the encoder (dominant kernel): algorithmic bytes per launch
+                   (2N read + S written per segment) / mean launch duration,
+                   against 8 TB/s; traffic = FETCH_SIZE + WRITE_SIZE bytes per
+                   launch from rocprofv3 (profiles/traffic_*.json, used only
+                   while the kernel source it was measured on is unchanged).
+  pcie             config 1 with the link: store = encode + kvszp_pack_streams
+                   into a pinned host slab, restore = one host-to-device copy
+                   + grouped decode (the reference's packed store and restore)
+  ratio            BF16 bytes / stream bytes of the step; ratio_uniform_1e-4:
+                   config 1's pages at a uniform REL 1e-4 (the metric's eb)
+  cpu_baseline     the scalar CPU oracle (C, -O2) on a sample of the same
+                   pages, store + restore, all host cores; one_core beside it;
+                   cpu_host_codecs: the reference's host codecs (zstd-1, LZ4,
+                   INT8), one core and all cores
 """
 
 from __future__ import annotations
 
 import argparse
 import ctypes
+import hashlib
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -40,181 +70,440 @@ sys.path.insert(0, PKG)
 
 METRIC = "KV compress/decompress GB/s (BF16 in), % of HBM peak, ratio at eb=1e-4"
 HBM_PEAK_GBPS = 8000.0
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_qwen15b_4k_store_restore.json")
+KERNELS_SRC = os.path.join(PKG, "csrc", "kvszp_kernels.hip")
+
+
+def traffic_file(config: int) -> str:
+    name = {1: "qwen15b_4k_store_restore"}.get(config, f"config{config}")
+    return os.path.join(REPO, "profiles", f"traffic_{name}.json")
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-class Workload:
-    """Config 1 pages, compressed slabs and pointer tables, built once."""
+def kernels_sha() -> str:
+    with open(KERNELS_SRC, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
 
-    def __init__(self, seed: int, tokens: int | None = None,
-                 grouped_restore: bool = True):
+
+# ---- workloads -------------------------------------------------------------------
+
+class Workload:
+    """Pages, stream slabs and destinations of one configuration, `sets`
+    copies at distinct addresses; pointer tables built once per set."""
+
+    grouped = False
+
+    def __init__(self, config: int, seed: int, sets: int):
+        import kvszp
         import torch
 
-        import kv_synth
-        import kvszp
-
-        self.kvszp = kvszp
-        self.shape = kv_synth.QWEN25_1P5B_4K
-        self.pages = kv_synth.paged_kv(self.shape, seed=seed, device="cuda",
-                                       tokens=tokens)
-        self.dest = torch.zeros_like(self.pages)
+        self.k = kvszp
+        self.torch = torch
+        self.config = config
+        self.build(seed)
         self.num_pages, self.page_numel = self.pages.shape
-        self.epl = self.shape.elements_per_layer
-        self.groups = kv_synth.mixed_bound_groups()
-        self.layer_idx = [torch.tensor(ls, dtype=torch.long, device="cuda")
-                          for _, ls in self.groups]
-        # requests group by group, page by page (the connector's order)
-        caps, eps, self.seg_numel = [], [], []
-        for bound, layers in self.groups:
-            n = 2 * len(layers) * self.epl
-            for _ in range(self.num_pages):
-                caps.append(8 * n)
-                eps.append(bound)
-                self.seg_numel.append(n)
-        self.batch = len(caps)
-        self.slab = torch.empty(sum(caps), dtype=torch.uint8, device="cuda")
-        offs = [0]
-        for c in caps[:-1]:
-            offs.append(offs[-1] + c)
-        base = self.slab.data_ptr()
-        page_ptrs = [p.data_ptr() for p in self.pages]
-        dest_ptrs = [p.data_ptr() for p in self.dest]
-        self.inputs = kvszp.ptr_array(page_ptrs * len(self.groups))
-        self.outputs = kvszp.ptr_array([base + o for o in offs])
-        self.stream_ptrs = [base + o for o in offs]
-        self.caps = kvszp.u64_array(caps)
-        self.eps = kvszp.f32_array(eps)
-        self.idx_ptrs = kvszp.ptr_array([t.data_ptr() for t in self.layer_idx])
-        self.sel = kvszp.size_array([len(ls) for _, ls in self.groups])
-        self.group_sizes = kvszp.size_array([self.num_pages] * len(self.groups))
-        self.dest_ptrs = kvszp.ptr_array(dest_ptrs)
-        self.sizes = (ctypes.c_uint64 * self.batch)()
-        self.bounds = (ctypes.c_float * self.batch)()
-        cfg = kvszp.Config(1e-4, 1, kvszp.DIM_1D, kvszp.MODE_FIXED,
-                           kvszp.TYPE_FLOAT)
+        cfg = kvszp.Config(1e-4, 1, kvszp.DIM_1D, kvszp.MODE_FIXED, kvszp.TYPE_FLOAT)
         self.ctx = kvszp.Context(cfg, 0)
         self.stream = torch.cuda.current_stream().cuda_stream
-        self.group_slices = []
-        start = 0
-        for _ in self.groups:
-            self.group_slices.append((start, start + self.num_pages))
-            start += self.num_pages
-        # Per-group restore arguments, built once like the other tables.
-        self.grouped_restore = grouped_restore
-        self.stream_table = kvszp.ptr_array(self.stream_ptrs)
-        # one destination page per request: every group restores into the
-        # same fresh pages
-        self.dest_table = kvszp.ptr_array(dest_ptrs * len(self.groups))
-        self.restore_args = []
-        for g, (lo, hi) in enumerate(self.group_slices):
-            cnt = hi - lo
-            self.restore_args.append((
-                kvszp.ptr_array(self.stream_ptrs[lo:hi]),
-                (ctypes.c_uint64 * cnt).from_buffer(self.sizes, lo * 8),
-                (ctypes.c_float * cnt).from_buffer(self.bounds, lo * 4),
-                cnt, self.layer_idx[g].data_ptr(), len(self.groups[g][1])))
+        self.sets = [self.make_set(s) for s in range(sets)]
 
-    def store(self) -> None:
-        k = self.kvszp
-        k.check(self.ctx.compress_indexed_groups(
-            self.inputs, self.outputs, self.caps, self.idx_ptrs, self.sel,
-            self.group_sizes, len(self.groups), 2, self.shape.layers, self.epl,
-            self.eps, self.batch, self.stream, self.sizes, self.bounds))
+    # requests: self.req_pages[i] (index of the input page), self.req_eps[i],
+    # self.req_n[i] (logical values); set up by build()
 
-    def restore(self) -> None:
-        k = self.kvszp
-        if self.grouped_restore:
-            k.check(self.ctx.decompress_indexed_scatter_groups(
-                self.stream_table, self.sizes, self.bounds, self.batch,
-                self.dest_table, self.idx_ptrs, self.sel, self.group_sizes,
-                len(self.groups), 2, self.shape.layers, self.epl,
-                self.stream))
-            return
-        for comp, sizes, bounds, cnt, idx, sel in self.restore_args:
-            k.check(self.ctx.decompress_indexed_scatter(
-                comp, sizes, bounds, cnt, self.dest_ptrs, idx, sel, 2,
-                self.shape.layers, self.epl, self.stream))
+    def make_set(self, s: int) -> dict:
+        torch, k = self.torch, self.k
+        pages = self.pages if s == 0 else self.pages.clone()
+        caps = [8 * n for n in self.req_n]
+        slab = torch.empty(sum(caps), dtype=torch.uint8, device="cuda")
+        offs, o = [], 0
+        for c in caps:
+            offs.append(o)
+            o += c
+        base = slab.data_ptr()
+        st = {
+            "pages": pages, "slab": slab,
+            "dest": torch.zeros_like(self.dest_template()),
+            "inputs": k.ptr_array([pages[p].data_ptr() for p in self.req_pages]),
+            "outputs": k.ptr_array([base + x for x in offs]),
+            "stream_ptrs": [base + x for x in offs],
+            "caps": k.u64_array(caps),
+            "eps": k.f32_array(self.req_eps),
+            "sizes": (ctypes.c_uint64 * len(caps))(),
+            "bounds": (ctypes.c_float * len(caps))(),
+        }
+        st["stream_table"] = k.ptr_array(st["stream_ptrs"])
+        self.make_restore_tables(st)
+        return st
 
-    def step(self) -> None:
-        self.store()
-        self.restore()
+    def dest_template(self):
+        return self.pages
+
+    @property
+    def batch(self) -> int:
+        return len(self.req_n)
 
     @property
     def bf16_bytes(self) -> int:
-        return 2 * self.num_pages * self.page_numel
+        return 2 * sum(self.req_n)
 
-    def stream_bytes(self) -> int:
-        return int(sum(self.sizes[i] for i in range(self.batch)))
+    def stream_bytes(self, s: int = 0) -> int:
+        st = self.sets[s]
+        return int(sum(st["sizes"][i] for i in range(self.batch)))
 
-
-def verify(w: Workload) -> dict:
-    """Round-trip checks on the measured data: restored pages within 2*eb of
-    the input on every element (the reference's BF16 tolerance, tests
-    :457, :639), and stream sizes/bounds consistent."""
-    import torch
-
-    err = (w.dest.float() - w.pages.float()).abs().view(
-        w.num_pages, 2, w.shape.layers, w.epl)
-    worst = 0.0
-    for g, (bound, layers) in enumerate(w.groups):
-        lo, hi = w.group_slices[g]
-        eb = torch.tensor([w.bounds[i] for i in range(lo, hi)], device="cuda")
-        e = err[:, :, list(layers)].amax(dim=(1, 2, 3))
-        worst = max(worst, float((e / (2 * eb + 1e-12)).max()))
-    return {"max_err_over_2eb": worst, "ok": worst <= 1.0}
+    def step(self, s: int) -> None:
+        self.store(s)
+        self.restore(s)
 
 
-def cpu_baseline(w: Workload, max_pages: int) -> dict:
-    """The scalar CPU oracle (one thread) on the same pages: store + restore
-    of `max_pages` pages, reported as BF16 GB/s like the GPU value."""
+class Grouped(Workload):
+    """Configs 1 and 4: layer groups by bound, one grouped indexed store and
+    one grouped indexed restore."""
+
+    grouped = True
+
+    def __init__(self, config, seed, sets, per_group_restore=False):
+        self.per_group_restore = per_group_restore
+        super().__init__(config, seed, sets)
+
+    def build(self, seed):
+        import kv_synth
+
+        torch = self.torch
+        if self.config == 1:
+            self.shape = kv_synth.QWEN25_1P5B_4K
+            self.pages = kv_synth.paged_kv(self.shape, seed=seed, device="cuda")
+            self.groups = kv_synth.mixed_bound_groups()
+            self.name = ("qwen2.5-1.5b 4k store+restore (configs[1]): 256 pages x "
+                         "[2,28,16,2,128] bf16, layers {0,1,2,5,19,20,21} REL 1e-5 + "
+                         "21 layers REL 1e-4, indexed_groups compress + "
+                         "indexed_scatter_groups restore")
+        else:
+            self.shape = kv_synth.LLAMA3_8B_64K
+            self.pages, self.classes = kv_synth.stress_pages(self.shape, seed=seed,
+                                                             device="cuda")
+            self.groups = kv_synth.alternating_bound_groups(self.shape.layers)
+            self.name = ("llama-3-8b 64k stress pages (configs[4]): 4096 pages x "
+                         "[2,32,16,8,128] bf16, per-layer REL 1e-4/1e-5 alternating, "
+                         "indexed_groups compress + indexed_scatter_groups restore")
+        self.epl = self.shape.elements_per_layer
+        npages = self.pages.shape[0]
+        self.req_pages, self.req_eps, self.req_n = [], [], []
+        for bound, layers in self.groups:
+            for p in range(npages):
+                self.req_pages.append(p)
+                self.req_eps.append(bound)
+                self.req_n.append(2 * len(layers) * self.epl)
+        self.layer_idx = [torch.tensor(ls, dtype=torch.long, device="cuda")
+                          for _, ls in self.groups]
+        k = __import__("kvszp")
+        self.idx_ptrs = k.ptr_array([t.data_ptr() for t in self.layer_idx])
+        self.sel = k.size_array([len(ls) for _, ls in self.groups])
+        self.group_sizes = k.size_array([npages] * len(self.groups))
+
+    def make_restore_tables(self, st):
+        k = self.k
+        dest_ptrs = [st["dest"][p].data_ptr() for p in range(self.num_pages)]
+        st["dest_table"] = k.ptr_array(dest_ptrs * len(self.groups))
+        st["per_group"] = []
+        for g in range(len(self.groups)):
+            lo, hi = g * self.num_pages, (g + 1) * self.num_pages
+            st["per_group"].append((
+                k.ptr_array(st["stream_ptrs"][lo:hi]),
+                (ctypes.c_uint64 * (hi - lo)).from_buffer(st["sizes"], lo * 8),
+                (ctypes.c_float * (hi - lo)).from_buffer(st["bounds"], lo * 4),
+                hi - lo, k.ptr_array(dest_ptrs), self.layer_idx[g].data_ptr(),
+                len(self.groups[g][1])))
+
+    def store(self, s):
+        st = self.sets[s]
+        self.k.check(self.ctx.compress_indexed_groups(
+            st["inputs"], st["outputs"], st["caps"], self.idx_ptrs, self.sel,
+            self.group_sizes, len(self.groups), 2, self.shape.layers, self.epl,
+            st["eps"], self.batch, self.stream, st["sizes"], st["bounds"]))
+
+    def restore(self, s):
+        st = self.sets[s]
+        if self.per_group_restore:
+            for comp, sizes, bounds, cnt, dests, idx, sel in st["per_group"]:
+                self.k.check(self.ctx.decompress_indexed_scatter(
+                    comp, sizes, bounds, cnt, dests, idx, sel, 2,
+                    self.shape.layers, self.epl, self.stream))
+            return
+        self.k.check(self.ctx.decompress_indexed_scatter_groups(
+            st["stream_table"], st["sizes"], st["bounds"], self.batch,
+            st["dest_table"], self.idx_ptrs, self.sel, self.group_sizes,
+            len(self.groups), 2, self.shape.layers, self.epl, self.stream))
+
+    def verify(self) -> dict:
+        """Restored values within 2*eb of the input on every element of the
+        restored layers (the reference's BF16 tolerance, tests :457, :639).
+        Constant pages (config 4) saturate the quantizer under a relative
+        bound (eb = eps * 1e-6) and are left out: the connector stores them
+        raw (vllm_v1_compressed_offload.py:994-1005)."""
+        torch = self.torch
+        st = self.sets[0]
+        err = (st["dest"].float() - self.pages.float()).abs().view(
+            self.num_pages, 2, self.shape.layers, self.epl)
+        keep = torch.tensor([c != "constant" for c in getattr(
+            self, "classes", ["gaussian"] * self.num_pages)], device="cuda")
+        worst = 0.0
+        for g, (_, layers) in enumerate(self.groups):
+            lo = g * self.num_pages
+            eb = torch.tensor([st["bounds"][lo + p] for p in range(self.num_pages)],
+                              device="cuda")
+            e = err[:, :, list(layers)].amax(dim=(1, 2, 3))
+            finite = torch.isfinite(e) & keep
+            worst = max(worst, float((e[finite] / (2 * eb[finite] + 1e-30)).max()))
+        return {"max_err_over_2eb": worst, "ok": worst <= 1.0}
+
+
+class Uniform(Workload):
+    """Configs 0, 2, 3: one bound for all pages, compress_batch_fixed_bf16,
+    restore contiguous (config 0) or into permuted fresh page slots."""
+
+    def build(self, seed):
+        import kv_synth
+
+        torch = self.torch
+        g = torch.Generator().manual_seed(seed + 17)
+        if self.config == 0:
+            shape = kv_synth.QWEN25_1P5B_4K
+            kk, vv = kv_synth.layer_kv(shape, layer=0, seed=seed, device="cuda")
+            self.pages = torch.stack([kk.reshape(-1), vv.reshape(-1)])
+            self.eps, self.slots = 1e-4, None
+            self.name = ("qwen2.5-1.5b single layer (configs[0]): K and V [4096,2,128] "
+                         "bf16 as 2 pages, REL 1e-4, compress_batch_fixed_bf16 + "
+                         "decompress_batch_fixed_bf16")
+        elif self.config == 2:
+            shape = kv_synth.QWEN25_1P5B_4K
+            pool = kv_synth.paged_kv(shape, seed=seed, device="cuda", tokens=16 * 8192)
+            order = torch.randperm(pool.shape[0], generator=g)
+            self.pool, self.order = pool, order
+            self.pages = pool
+            self.eps = 1e-4
+            self.slots = torch.randperm(pool.shape[0], generator=g).tolist()
+            self.name = ("qwen2.5-1.5b 16x8k pool (configs[2]): 8192 pages x "
+                         "[2,28,16,2,128] bf16 in page-table order, REL 1e-4, "
+                         "compress_batch_fixed_bf16 + scatter restore to permuted slots")
+        else:
+            shape = kv_synth.QWEN25_7B_32K
+            self.pages = kv_synth.rope_kv(shape, seed=seed, device="cuda")
+            self.eps = 1e-5
+            self.slots = torch.randperm(self.pages.shape[0], generator=g).tolist()
+            self.name = ("qwen2.5-7b 32k (configs[3]): 2048 pages x [2,28,16,4,128] "
+                         "bf16, RoPE-like K, REL 1e-5, compress_batch_fixed_bf16 + "
+                         "scatter restore to permuted slots")
+        npages, n = self.pages.shape
+        if self.config == 2:
+            self.req_pages = self.order.tolist()
+        else:
+            self.req_pages = list(range(npages))
+        self.req_eps = [self.eps] * npages
+        self.req_n = [n] * npages
+
+    def make_restore_tables(self, st):
+        k = self.k
+        if self.slots is None:
+            return
+        st["slot_table"] = k.ptr_array([st["dest"][s].data_ptr() for s in self.slots])
+
+    def store(self, s):
+        st = self.sets[s]
+        self.k.check(self.ctx.compress(
+            st["inputs"], st["outputs"], st["caps"], st["eps"], self.batch,
+            self.page_numel, self.stream, st["sizes"], st["bounds"]))
+
+    def restore(self, s):
+        st = self.sets[s]
+        if self.slots is None:
+            self.k.check(self.ctx.decompress(
+                st["stream_table"], st["sizes"], st["bounds"], self.batch,
+                st["dest"].data_ptr(), st["dest"].numel(), self.page_numel,
+                self.stream))
+            return
+        self.k.check(self.ctx.decompress_scatter(
+            st["stream_table"], st["sizes"], st["bounds"], self.batch,
+            st["slot_table"], self.page_numel, 1, self.page_numel, self.stream))
+
+    def verify(self) -> dict:
+        torch = self.torch
+        st = self.sets[0]
+        src = self.pages[self.req_pages] if self.config == 2 else self.pages
+        out = st["dest"] if self.slots is None else st["dest"][self.slots]
+        e = (out.float() - src.float()).abs().amax(dim=1)
+        eb = torch.tensor([st["bounds"][i] for i in range(self.batch)], device="cuda")
+        finite = torch.isfinite(e)
+        worst = float((e[finite] / (2 * eb[finite] + 1e-30)).max())
+        return {"max_err_over_2eb": worst, "ok": worst <= 1.0}
+
+
+def make_workload(config: int, seed: int, sets: int, per_group_restore: bool):
+    if config in (1, 4):
+        return Grouped(config, seed, sets, per_group_restore)
+    return Uniform(config, seed, sets)
+
+
+# ---- measurement --------------------------------------------------------------------
+
+def kernel_stats(ms: list) -> dict:
+    if not ms:
+        return {}
+    return {"mean_ms": round(statistics.fmean(ms), 5), "min_ms": round(min(ms), 5),
+            "median_ms": round(statistics.median(ms), 5), "launches": len(ms)}
+
+
+def timed_steps(w: Workload, steps: int, sets: int) -> dict:
+    """K steps over `sets` buffer sets: wall time, then the encoder's and the
+    decoder's per-launch durations (each from its own pass of K steps; an
+    event pair costs a little GPU time, so only one kind is timed at once)."""
+    torch, k = w.torch, w.k
+    torch.cuda.synchronize()
+    w.ctx.enable_timing(0)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        w.step(i % sets)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    out = {"ms_per_step": wall / steps * 1e3}
+    for kind, key in ((k.KERNEL_COMPRESS, "compress"), (k.KERNEL_DECOMPRESS, "decompress")):
+        w.ctx.timing_durations(kind)
+        w.ctx.enable_timing(1 << kind)
+        for i in range(steps):
+            w.step(i % sets)
+        torch.cuda.synchronize()
+        w.ctx.enable_timing(0)
+        ms = w.ctx.timing_durations(kind)
+        per_step = len(ms) // steps if steps else 0
+        out[key] = kernel_stats(ms)
+        out[key]["launches_per_step"] = per_step
+        # a step's kernel time (several launches per step: one per 16 groups)
+        out[key]["ms_per_step"] = sum(ms) / steps if steps else 0.0
+    return out
+
+
+def pcie_steps(w: Grouped, steps: int) -> dict:
+    """Config 1 across the link: store = encode + pack into a pinned slab
+    (blocking, like put_many_packed), restore = one host-to-device copy +
+    grouped decode; `steps` steps on buffer set 0."""
+    torch, k = w.torch, w.k
+    st = w.sets[0]
+    w.store(0)
+    sizes = [st["sizes"][i] for i in range(w.batch)]
+    cap = sum(sizes) + 8 * w.batch + (64 << 20)
+    slab = torch.empty(cap, dtype=torch.uint8).pin_memory()
+    staging = torch.empty(cap, dtype=torch.uint8, device="cuda")
+    offsets = (ctypes.c_uint64 * w.batch)()
+    packed = ctypes.c_uint64()
+    lens = (ctypes.c_uint64 * w.batch)()
+    t_store = t_restore = 0.0
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        w.store(0)
+        for i in range(w.batch):
+            lens[i] = st["sizes"][i]
+        k.check(w.ctx.pack(st["stream_table"], lens, w.batch, slab.data_ptr(), cap,
+                           w.stream, offsets, ctypes.byref(packed)))
+        t1 = time.perf_counter()
+        k.check(w.ctx.decompress_indexed_scatter_groups_packed(
+            slab.data_ptr(), packed.value, staging.data_ptr(), cap, offsets, lens,
+            st["bounds"], w.batch, st["dest_table"], w.idx_ptrs, w.sel, w.group_sizes,
+            len(w.groups), 2, w.shape.layers, w.epl, w.stream))
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        t_store += t1 - t0
+        t_restore += t2 - t1
+    b = w.bf16_bytes
+    return {"store_restore_gbps": round(b * steps / (t_store + t_restore) / 1e9, 2),
+            "store_gbps": round(b * steps / t_store / 1e9, 2),
+            "restore_gbps": round(b * steps / t_restore / 1e9, 2),
+            "ms_per_step": round((t_store + t_restore) / steps * 1e3, 4),
+            "packed_bytes": int(packed.value), "steps": steps,
+            "link_gbps": round(2 * packed.value * steps / (t_store + t_restore) / 1e9, 2)}
+
+
+def uniform_ratio(w: Grouped) -> float:
+    """Config 1's pages at a uniform REL 1e-4 (the metric's eb): one
+    compress_batch_fixed_bf16 call over the 256 whole pages."""
+    torch, k = w.torch, w.k
+    n = w.page_numel
+    slab = torch.empty(w.num_pages * 8 * n, dtype=torch.uint8, device="cuda")
+    sizes = (ctypes.c_uint64 * w.num_pages)()
+    bounds = (ctypes.c_float * w.num_pages)()
+    k.check(w.ctx.compress(
+        k.ptr_array([w.pages[p].data_ptr() for p in range(w.num_pages)]),
+        k.ptr_array([slab.data_ptr() + p * 8 * n for p in range(w.num_pages)]),
+        k.u64_array([8 * n] * w.num_pages), k.f32_array([1e-4] * w.num_pages),
+        w.num_pages, n, w.stream, sizes, bounds))
+    return round(2 * n * w.num_pages / sum(sizes), 4)
+
+
+def host_info() -> dict:
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"nproc": cores, "cpu_model": model}
+
+
+def cpu_baseline(w: Grouped, max_pages: int, threads: int) -> dict:
+    """The scalar CPU oracle on config 1's first `max_pages` pages, store +
+    restore of both layer groups, on `threads` threads and on one."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
 
-    import torch
-
-    host = w.pages[:max_pages].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
-    n_pages = host.shape[0]
-    t_c = t_d = 0.0
-    for bound, layers in w.groups:
-        streams, sizes, bounds, enc_s = oracle.compress_batch(
-            host, [bound] * n_pages, relative=True, threads=1,
-            layer_indices=list(layers), source_layers=w.shape.layers,
-            elements_per_layer=w.epl, return_elapsed=True)
-        n = 2 * len(layers) * w.epl
-        out = np.zeros_like(host)
-        t1 = time.perf_counter()
-        for i in range(n_pages):
-            oracle.decompress_indexed(streams[i], n, float(bounds[i]), out[i],
-                                      list(layers), w.shape.layers, w.epl)
-        t2 = time.perf_counter()
-        t_c += enc_s
-        t_d += t2 - t1
+    host = w.pages[:max_pages].contiguous().cpu().view(w.torch.int16).numpy().view(np.uint16)
     nbytes = 2 * host.size
-    return {"value": round(nbytes / (t_c + t_d) / 1e9, 4), "unit": "GB/s",
-            "cores": 1, "kind": "port",
-            "sample": f"{n_pages} of 256 pages (both layer groups), store+restore",
-            "compress_gbps": round(nbytes / t_c / 1e9, 4),
-            "decompress_gbps": round(nbytes / t_d / 1e9, 4)}
+
+    def run(nthreads):
+        t_c = t_d = 0.0
+        for bound, layers in w.groups:
+            streams, sizes, bounds, enc_s = oracle.compress_batch(
+                host, [bound] * host.shape[0], relative=True, threads=nthreads,
+                layer_indices=list(layers), source_layers=w.shape.layers,
+                elements_per_layer=w.epl, return_elapsed=True)
+            out = np.zeros_like(host)
+            n = 2 * len(layers) * w.epl
+            t1 = time.perf_counter()
+            oracle.decompress_batch_indexed(streams, sizes, n, bounds, out, list(layers),
+                                            w.shape.layers, w.epl, threads=nthreads)
+            t_d += time.perf_counter() - t1
+            t_c += enc_s
+        return {"value": round(nbytes / (t_c + t_d) / 1e9, 4), "unit": "GB/s",
+                "cores": nthreads,
+                "compress_gbps": round(nbytes / t_c / 1e9, 4),
+                "decompress_gbps": round(nbytes / t_d / 1e9, 4)}
+
+    one = run(1)
+    allc = run(threads) if threads > 1 else dict(one)
+    allc.update({"kind": "port",
+                 "sample": f"{host.shape[0]} of 256 config-1 pages, both layer groups, "
+                           "store+restore (oracle/kvszp_oracle.c, gcc -O2)",
+                 "one_core": one})
+    return allc
 
 
-def host_codec_baselines(w: Workload, max_pages: int) -> dict:
-    """The reference's host codecs (zstd level 1, LZ4 default, INT8) on the
-    same BF16 page bytes, one thread, as reported extras."""
+def host_codec_baselines(w: Grouped, max_pages: int, threads: int) -> dict:
     import numpy as np
-    import torch
 
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import cpu_codecs
 
-    host = w.pages[:max_pages].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
-    return cpu_codecs.time_all(host)
+    host = w.pages[:max_pages].contiguous().cpu().view(w.torch.int16).numpy().view(np.uint16)
+    return cpu_codecs.time_all(host, threads=threads)
 
+
+# ---- rocprof traffic post-processing (no GPU) ----------------------------------------
 
 def _pmc_per_dispatch(run_dir: str, counter: str) -> dict:
     """{kernel kind: [value per dispatch, KiB]} from a rocprofv3 --pmc CSV."""
@@ -235,9 +524,9 @@ def _pmc_per_dispatch(run_dir: str, counter: str) -> dict:
     for did in sorted(per):
         name = names[did]
         if "kvszp::" in name and "decompress" in name:
-            kind = "decompress_kernel"   # decompress_kernel / decompress_persistent_kernel
+            kind = "decompress_kernel"
         elif "kvszp::" in name and "compress" in name and "minmax" not in name:
-            kind = "compress_kernel"     # compress_kernel / compress_persistent_kernel
+            kind = "compress_kernel"
         elif "copyBuffer" in name:
             kind = "copy"
         else:
@@ -246,10 +535,10 @@ def _pmc_per_dispatch(run_dir: str, counter: str) -> dict:
     return out
 
 
-def traffic_from(base: str) -> int:
+def traffic_from(base: str, config: int) -> int:
     """HBM bytes per launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch),
     each scaled so that a plain device copy of known size reads and writes
-    exactly its own bytes."""
+    exactly its own bytes; written with the kernel source's hash."""
     with open(os.path.join(base, "copy_calibration.json")) as f:
         copy_bytes = json.load(f)["copy_bytes_each_way"]
     cf = _pmc_per_dispatch(os.path.join(base, "copy_fetch"), "FETCH_SIZE")["copy"]
@@ -259,50 +548,88 @@ def traffic_from(base: str) -> int:
     bf = _pmc_per_dispatch(os.path.join(base, "bench_fetch"), "FETCH_SIZE")
     bw = _pmc_per_dispatch(os.path.join(base, "bench_write"), "WRITE_SIZE")
     result = {"fetch_factor": round(fetch_factor, 4),
-              "write_factor": round(write_factor, 4)}
+              "write_factor": round(write_factor, 4),
+              "kernels_sha": kernels_sha()}
     for kind in ("compress_kernel", "decompress_kernel"):
         fetch = sum(bf[kind]) / len(bf[kind]) * 1024 * fetch_factor
         write = sum(bw[kind]) / len(bw[kind]) * 1024 * write_factor
         result[kind] = int(round(fetch + write))
         result[kind + "_fetch"] = int(round(fetch))
         result[kind + "_write"] = int(round(write))
-    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
-    with open(TRAFFIC_FILE, "w") as f:
+    path = traffic_file(config)
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    with open(path, "w") as f:
         json.dump(result, f, indent=1)
     print(json.dumps(result))
     return 0
 
 
+def bw_probe(sets: int = 4) -> dict:
+    """Achievable HBM rate of plain device copies (torch copy_), read + write
+    bytes per second, on buffers rotated so that a copy reads nothing the
+    Infinity Cache holds, and on one buffer pair (cache-warm)."""
+    import torch
+
+    out = {}
+    for mib in (64, 117, 256, 1024):
+        n = (mib << 20) // 2
+        srcs = [torch.ones(n, dtype=torch.bfloat16, device="cuda") for _ in range(sets)]
+        dsts = [torch.empty_like(s) for s in srcs]
+        res = {}
+        for label, rot in (("cold", sets), ("warm", 1)):
+            ts = []
+            for r in range(24):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                dsts[r % rot].copy_(srcs[r % rot])
+                b.record()
+                b.synchronize()
+                ts.append(a.elapsed_time(b))
+            ms = statistics.median(ts[4:])
+            res[label] = round(2 * n * 2 / (ms * 1e-3) / 1e9, 1)
+        out[f"{mib}MiB"] = res
+        del srcs, dsts
+        torch.cuda.empty_cache()
+    return out
+
+
+# ---- main ---------------------------------------------------------------------------
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    # A step is ~0.12 ms: 200 timed steps (~25 ms of GPU time) give a steady
-    # state; 20 steps read ~5 % low from first-step effects.
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4))
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 200 for configs 0/1, 20 otherwise)")
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--rotate", type=int, default=None,
+                    help="buffer sets the steps rotate through (default 3 for "
+                         "configs 0/1, 1 otherwise)")
     ap.add_argument("--cpu-pages", type=int, default=256,
-                    help="pages of the CPU baseline sample")
+                    help="config-1 pages of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-pcie", action="store_true")
     ap.add_argument("--restore-per-group", action="store_true",
-                    help="restore with one indexed_scatter call per layer "
-                         "group (the reference's call pattern) instead of "
-                         "one grouped launch")
+                    help="grouped configs: one indexed_scatter call per layer group "
+                         "(the reference's call pattern) instead of one grouped launch")
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a plain 256 MiB device copy (the reference "
-                         "kernel for scaling rocprof FETCH_SIZE/WRITE_SIZE)")
+                    help="only run a plain 256 MiB device copy (the reference kernel "
+                         "for scaling rocprof FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--bw-probe", action="store_true",
+                    help="only measure plain device-copy rates (cache-cold and warm)")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="no GPU work: turn the rocprofv3 --pmc runs under DIR "
-                         "(copy_fetch, copy_write, bench_fetch, bench_write) into "
-                         "HBM bytes per launch, written to " + TRAFFIC_FILE)
+                         "(copy_fetch, copy_write, bench_fetch, bench_write) into HBM "
+                         "bytes per launch for --config")
     args = ap.parse_args()
     if args.traffic_from:
-        return traffic_from(args.traffic_from)
+        return traffic_from(args.traffic_from, args.config)
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(KV pages are private to the GPU that owns them; see DESIGN.md "
-              "for how the path shards).", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (KV pages "
+              "are private to the GPU that owns them; see DESIGN.md for how the "
+              "path shards).", file=sys.stderr)
         return 2
 
     import torch
@@ -314,118 +641,109 @@ def main() -> int:
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes_each_way": src.numel() * 2,
-                          "copies": 3}), flush=True)
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 2, "copies": 3}), flush=True)
         return 0
-    log("building workload")
-    w = Workload(args.seed, grouped_restore=not args.restore_per_group)
-    log(f"workload: {w.num_pages} pages x {w.page_numel} BF16, "
-        f"{w.batch} segment requests")
-    for _ in range(max(1, args.warmup)):
-        w.step()
+    if args.bw_probe:
+        print(json.dumps({"bw_probe_gbps_read_plus_write": bw_probe()}), flush=True)
+        return 0
+
+    small = args.config in (0, 1)
+    steps = args.steps if args.steps is not None else (200 if small else 20)
+    warmup = args.warmup if args.warmup is not None else (20 if small else 3)
+    sets = args.rotate if args.rotate is not None else (3 if small else 1)
+    log(f"building config {args.config} ({sets} buffer sets)")
+    w = make_workload(args.config, args.seed, sets, args.restore_per_group)
+    log(f"{w.num_pages} pages x {w.page_numel} BF16, {w.batch} requests")
+    for i in range(max(1, warmup)):
+        w.step(i % sets)
     torch.cuda.synchronize()
-    check = verify(w)
+    check = w.verify()
     log(f"round trip check: {check}")
     if not check["ok"]:
         print("error bound violated", file=sys.stderr)
         return 1
-    ratio = w.bf16_bytes / w.stream_bytes()
+    s_bytes = w.stream_bytes(0)
+    ratio = w.bf16_bytes / s_bytes
 
-    # Timed region: whole steps, with HIP events around the dominant kernel
-    # (the encoder) only -- each event record costs GPU time.
-    w.ctx.drain_timing()
-    w.ctx.enable_timing(w.kvszp.TIME_COMPRESS)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        w.step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    w.ctx.enable_timing(0)
-    kt = w.ctx.drain_timing()
-    step_s = (t1 - t0) / args.steps
-    # Decoder launch durations from a second pass of the same steps (not
-    # part of `value`).
-    w.ctx.enable_timing(w.kvszp.TIME_DECOMPRESS)
-    for _ in range(args.steps):
-        w.step()
-    torch.cuda.synchronize()
-    w.ctx.enable_timing(0)
-    dt = w.ctx.drain_timing()
-    kt["decompress_ms"] = dt["decompress_ms"]
-    dec_launches = max(1, dt["decompress_launches"] // max(1, args.steps))
-
-    # Algorithmic bytes per launch: compress reads 2N and writes S per
-    # segment; restore reads S and writes 2N.
-    s_bytes = w.stream_bytes()
-    comp_launch_bytes = w.bf16_bytes + s_bytes
-    comp_ms = kt["compress_ms"] / max(1, kt["compress_launches"])
-    dec_ms_step = kt["decompress_ms"] / args.steps
-    comp_gbps = w.bf16_bytes / (comp_ms * 1e-3) / 1e9
-    dec_gbps = w.bf16_bytes / (dec_ms_step * 1e-3) / 1e9
-    comp_hbm = comp_launch_bytes / (comp_ms * 1e-3) / 1e9
-    dec_hbm = (w.bf16_bytes + s_bytes) / (dec_ms_step * 1e-3) / 1e9
-    if comp_ms >= dec_ms_step:
-        dom = ("compress_kernel", comp_hbm, comp_launch_bytes)
-    else:
-        dom = ("decompress_kernel", dec_hbm,
-               (w.bf16_bytes + s_bytes) / dec_launches)
+    cold = timed_steps(w, steps, sets)
+    warm = timed_steps(w, steps, 1) if sets > 1 else cold
+    step_ms = cold["ms_per_step"]
+    enc, dec = cold["compress"], cold["decompress"]
+    enc_launch_bytes = (w.bf16_bytes + s_bytes) / max(1, enc["launches_per_step"])
+    enc_hbm = enc_launch_bytes / (enc["mean_ms"] * 1e-3) / 1e9
+    dec_hbm = (w.bf16_bytes + s_bytes) / (dec["ms_per_step"] * 1e-3) / 1e9
     traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get(dom[0])
+    tf = traffic_file(args.config)
+    if os.path.exists(tf):
+        with open(tf) as f:
+            t = json.load(f)
+        if t.get("kernels_sha") == kernels_sha():
+            traffic = t.get("compress_kernel")
 
     result = {
         "metric": METRIC,
-        "value": round(w.bf16_bytes / step_s / 1e9, 3),
+        "value": round(w.bf16_bytes / (step_ms * 1e-3) / 1e9, 3),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(step_s * 1e3, 4),
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(step_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": "qwen2.5-1.5b 4k store+restore (configs[1]): 256 pages "
-                        "x [2,28,16,2,128] bf16, layers {0,1,2,5,19,20,21} REL "
-                        "1e-5 + 21 layers REL 1e-4, indexed_groups compress + "
-                        + ("2x indexed_scatter restore" if args.restore_per_group
-                           else "indexed_scatter_groups restore"),
+            "workload": w.name + (" (per-group restore)" if args.restore_per_group else ""),
+            "config_index": args.config,
             "pages": w.num_pages,
             "page_elements": w.page_numel,
             "segment_requests": w.batch,
             "kv_bytes": w.bf16_bytes,
+            "buffer_sets": sets,
             "parallelism": "single GPU",
         },
+        "value_mall_warm": round(w.bf16_bytes / (warm["ms_per_step"] * 1e-3) / 1e9, 3),
         "ratio": round(ratio, 4),
-        "compress_gbps": round(comp_gbps, 2),
-        "decompress_gbps": round(dec_gbps, 2),
-        "compress_kernel_ms": round(comp_ms, 4),
-        "decompress_kernel_ms_per_step": round(dec_ms_step, 4),
-        "compress_hbm_frac": round(comp_hbm / HBM_PEAK_GBPS, 4),
+        "compress_gbps": round(w.bf16_bytes / (enc["ms_per_step"] * 1e-3) / 1e9, 2),
+        "decompress_gbps": round(w.bf16_bytes / (dec["ms_per_step"] * 1e-3) / 1e9, 2),
+        "compress_kernel": enc,
+        "decompress_kernel": dec,
+        "compress_hbm_frac": round(enc_hbm / HBM_PEAK_GBPS, 4),
         "decompress_hbm_frac": round(dec_hbm / HBM_PEAK_GBPS, 4),
+        "mall_warm": {"compress_kernel": warm["compress"],
+                      "decompress_kernel": warm["decompress"],
+                      "ms_per_step": round(warm["ms_per_step"], 4)},
         "roofline": {
-            "kernel": dom[0],
+            "kernel": "compress_kernel",
             "bound": "hbm",
-            "achieved": round(dom[1], 2),
+            "achieved": round(enc_hbm, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(dom[1] / HBM_PEAK_GBPS, 4),
+            "frac": round(enc_hbm / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "algorithmic_bytes_per_launch": int(dom[2]),
+            "algorithmic_bytes_per_launch": int(enc_launch_bytes),
         },
+        "reencoded_calls": w.ctx.reencode_count(),
         "round_trip_check": check,
     }
-    if not args.no_cpu:
-        log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(w, args.cpu_pages)
-        try:
-            result["cpu_host_codecs"] = host_codec_baselines(w, min(args.cpu_pages, 64))
-        except Exception as exc:  # system codec libraries may be absent
-            result["cpu_host_codecs"] = {"error": str(exc)}
+    if args.config == 1:
+        result["ratio_uniform_1e-4"] = uniform_ratio(w)
+        if not args.no_pcie:
+            log("pcie store+restore")
+            result["pcie"] = pcie_steps(w, 20)
+        if not args.no_cpu:
+            info = host_info()
+            # the GPU box's share of host cores is 16, whatever nproc says
+            threads = max(1, min(info["nproc"] or 1, 16))
+            log(f"cpu baseline ({threads} threads)")
+            result["cpu_baseline"] = cpu_baseline(w, args.cpu_pages, threads)
+            result["cpu_baseline"].update(info)
+            try:
+                result["cpu_host_codecs"] = host_codec_baselines(
+                    w, min(args.cpu_pages, 64), threads)
+            except Exception as exc:  # system codec libraries may be absent
+                result["cpu_host_codecs"] = {"error": str(exc)}
     print(json.dumps(result), flush=True)
     return 0
 

@@ -295,6 +295,13 @@ int kvszp_enable_timing(kvszp_ctx* ctx, int kinds);
 int kvszp_drain_timing(kvszp_ctx* ctx, double* compress_ms, int* compress_count,
                        double* decompress_ms, int* decompress_count);
 
+/* The durations (milliseconds, launch order) of the timed launches of one
+ * kernel kind (KVSZP_KERNEL_*) recorded since they were last drained; at
+ * most `capacity` are written, *count_out says how many.  Those records are
+ * forgotten, records of the other kind are kept.  No reference counterpart. */
+int kvszp_timing_durations(kvszp_ctx* ctx, int kind, double* ms_out,
+                           int capacity, int* count_out);
+
 /* How many compress calls of this context were encoded a second time, with
  * the schedule that needs no residency (min/max pre-pass, one workgroup per
  * tile), because a launch's time-bounded cross-workgroup wait gave up (the

@@ -377,6 +377,32 @@ int kvo_decompress_batch_contiguous(const uint8_t* const* streams,
     return status ? -1 : 0;
 }
 
+/* Indexed restore of a batch (the reference's indexed scatter decode,
+ * cu:539-565): page p's segment to destinations[p], pages split across
+ * `threads` OpenMP threads (for the CPU baseline). */
+int kvo_decompress_batch_indexed(const uint8_t* const* streams,
+                                 const uint64_t* sizes, uint64_t batch,
+                                 uint64_t n, const float* bounds,
+                                 int rate0_policy, int threads,
+                                 uint16_t* const* destinations,
+                                 const int64_t* layer_indices,
+                                 uint64_t selected_layers, uint64_t source_layers,
+                                 uint64_t elements_per_layer) {
+    int status = 0;
+    int64_t p;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1) reduction(|: status)
+#endif
+    for (p = 0; p < (int64_t)batch; ++p)
+        status |= kvo_decompress_indexed(streams[p], sizes[p], n, bounds[p],
+                                          rate0_policy, destinations[p],
+                                          layer_indices, selected_layers,
+                                          source_layers, elements_per_layer)
+                  ? 1 : 0;
+    (void)threads;
+    return status ? -1 : 0;
+}
+
 /* ---- INT8 host codec --------------------------------------------------
  * vllm_v1_compressed_offload.py:711-724 runs on BF16 tensors, so every torch
  * op result is rounded to BF16:

@@ -94,6 +94,15 @@ int kvo_decompress_batch_contiguous(const uint8_t* const* streams,
                                     int rate0_policy, int threads,
                                     uint16_t* out);
 
+int kvo_decompress_batch_indexed(const uint8_t* const* streams,
+                                 const uint64_t* sizes, uint64_t batch,
+                                 uint64_t n, const float* bounds,
+                                 int rate0_policy, int threads,
+                                 uint16_t* const* destinations,
+                                 const int64_t* layer_indices,
+                                 uint64_t selected_layers, uint64_t source_layers,
+                                 uint64_t elements_per_layer);
+
 /* INT8 host codec (vllm_v1_compressed_offload.py:711-724, 2090-2123). */
 float kvo_int8_encode(const uint16_t* page, uint64_t n, int8_t* q);
 void kvo_int8_decode(const int8_t* q, uint64_t n, float scale, uint16_t* out);

@@ -101,6 +101,11 @@ def lib() -> ctypes.CDLL:
         L.kvo_decompress_f32.argtypes = [
             ctypes.c_void_p, _u64, _u64, ctypes.c_float, ctypes.c_int,
             ctypes.c_void_p]
+        L.kvo_decompress_batch_indexed.restype = ctypes.c_int
+        L.kvo_decompress_batch_indexed.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, _u64, _u64, ctypes.c_void_p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, _u64,
+            _u64, _u64]
         L.kvo_int8_encode.restype = ctypes.c_float
         L.kvo_int8_encode.argtypes = [ctypes.c_void_p, _u64, ctypes.c_void_p]
         L.kvo_int8_decode.restype = None
@@ -309,6 +314,28 @@ def decompress_f32(stream, n: int, eb: float,
     if rc != 0:
         raise ValueError("malformed fixed-mode stream")
     return out
+
+
+def decompress_batch_indexed(streams, sizes, n: int, bounds, out: np.ndarray,
+                             layer_indices, source_layers: int,
+                             elements_per_layer: int, threads: int = 1,
+                             rate0_policy: int = RATE0_ZERO) -> None:
+    """Decode stream p into the full page out[p] (uint16, [B, page_numel])
+    through the layer map, pages split across `threads` threads."""
+    batch = len(streams)
+    streams = [np.ascontiguousarray(s, dtype=np.uint8) for s in streams]
+    sp = (ctypes.c_void_p * batch)(*[s.ctypes.data for s in streams])
+    sz = np.ascontiguousarray(np.asarray(sizes, dtype=np.uint64))
+    eb = np.ascontiguousarray(np.asarray(bounds, dtype=np.float32))
+    dp = (ctypes.c_void_p * batch)(
+        *[out.ctypes.data + i * out.strides[0] for i in range(batch)])
+    idx, p = _layer_args(layer_indices)
+    rc = lib().kvo_decompress_batch_indexed(sp, sz.ctypes.data, batch, n,
+                                            eb.ctypes.data, rate0_policy, threads,
+                                            dp, p, idx.size, source_layers,
+                                            elements_per_layer)
+    if rc != 0:
+        raise ValueError("malformed fixed-mode stream")
 
 
 def int8_encode(page) -> tuple[np.ndarray, float]:

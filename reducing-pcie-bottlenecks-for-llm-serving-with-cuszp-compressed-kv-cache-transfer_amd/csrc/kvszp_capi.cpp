@@ -102,7 +102,7 @@ struct kvszp_ctx {
     unsigned long long* control = nullptr;
     unsigned long long ticket_next = 0;
     uint32_t epoch = 0;
-    DevBuf tile_state, tile_minmax, job_minmax, tables;
+    DevBuf tile_state, tile_minmax, job_minmax, job_flags, tables;
     StagingSlot slots[kSlots];
     int next_slot = 0;
     uint32_t seq = 0;                     // last launch sequence number
@@ -113,7 +113,7 @@ struct kvszp_ctx {
     // pinned host areas of fixed size, all set up by kvszp_create.
     unsigned char* scratch = nullptr;
     CompressJob* noalloc_stage = nullptr;     // kNoAllocMaxJobs job records
-    void* noalloc_results = nullptr;          // kNoAllocMaxJobs sizes + bounds
+    void* noalloc_results = nullptr;          // kNoAllocMaxJobs sizes, bounds, redo marks
     // Optional kernel timing: event pairs recorded on the launch stream for
     // the kernel kinds in the mask (bit KVSZP_KERNEL_*).
     int timing = 0;
@@ -178,6 +178,7 @@ int ensure_host_results(kvszp_ctx* c, size_t bytes) {
     const size_t grown = std::max<size_t>(bytes, 4096);
     hipError_t e = hipHostMalloc(&c->host_results, grown, hipHostMallocCoherent);
     if (e != hipSuccess) return fail(KVSZP_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
+    std::memset(c->host_results, 0, grown);  // no stale redo marks
     c->host_results_bytes = grown;
     return KVSZP_OK;
 }
@@ -244,7 +245,8 @@ int upload_tables(kvszp_ctx* c, const void* data, size_t bytes, uint32_t seq,
 // Next epoch tag; on wrap-around all tagged words are cleared first.
 int next_epoch(kvszp_ctx* c, hipStream_t stream, uint32_t* epoch) {
     if (c->epoch >= kEpochLimit) {
-        DevBuf* bufs[3] = {&c->tile_state, &c->tile_minmax, &c->job_minmax};
+        DevBuf* bufs[4] = {&c->tile_state, &c->tile_minmax, &c->job_minmax,
+                           &c->job_flags};
         for (DevBuf* b : bufs) {
             if (!b->ptr) continue;
             hipError_t e = hipMemsetAsync(b->ptr, 0, b->bytes, stream);
@@ -398,11 +400,14 @@ int fill_groups(Group* groups, const std::vector<GroupSpec>& specs, const Chunk&
 // Common compress path: `specs` are the groups, requests laid out group by
 // group in inputs/outputs.  `f32`: contiguous fp32 pages (the single-page
 // API, cuszp_wrapper.cpp:216-429) instead of BF16 pages.
+// `safe`: only the schedule that needs no residency (pre-pass bound, one
+// workgroup per tile).
 int compress_groups(kvszp_ctx* c, const void* const* inputs,
                     void* const* outputs, const uint64_t* capacities,
                     const float* eps_overrides, size_t batch,
                     const std::vector<GroupSpec>& specs, hipStream_t stream,
-                    uint64_t* sizes_out, float* bounds_out, bool f32 = false) {
+                    uint64_t* sizes_out, float* bounds_out, bool f32 = false,
+                    bool safe = false) {
     int rc = check_fixed_config(c);
     if (rc) return rc;
     if (batch == 0) return fail(KVSZP_EINVAL, "empty batch");
@@ -467,7 +472,8 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     if ((rc = ensure(c->tile_state, max_tiles * 8, true, stream)) ||
         (rc = ensure(c->tile_minmax, max_tiles * 8, true, stream)) ||
         (rc = ensure(c->job_minmax, batch * 16, true, stream)) ||
-        (rc = ensure_host_results(c, batch * 8)))
+        (rc = ensure(c->job_flags, batch * 4, true, stream)) ||
+        (rc = ensure_host_results(c, batch * 12)))
         return rc;
     const uint32_t seq = ++c->seq;
     rc = upload_tables(c, jobs.data(), batch * sizeof(CompressJob), seq, stream);
@@ -475,6 +481,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
 
     uint32_t* host_sizes = reinterpret_cast<uint32_t*>(c->host_results);
     float* host_bounds = reinterpret_cast<float*>(host_sizes + batch);
+    uint32_t* host_redo = host_sizes + 2 * batch;
     const CompressJob* djobs = reinterpret_cast<const CompressJob*>(c->tables.ptr);
 
     // One launch per chunk (normally one); all share the call's sequence
@@ -525,6 +532,8 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         p.job_minmax = reinterpret_cast<const unsigned long long*>(c->job_minmax.ptr);
         p.host_sizes = host_sizes;
         p.host_bounds = host_bounds;
+        p.host_redo = host_redo;
+        p.job_flags = reinterpret_cast<uint32_t*>(c->job_flags.ptr);
         p.error = error_word(c);
         p.host_ctl = c->host_ctl;
         p.seq = seq;
@@ -562,18 +571,16 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         return KVSZP_OK;
     };
     for (size_t k = 0; k < chunks.size(); ++k)
-        if ((rc = launch_chunk(k, false))) return rc;
+        if ((rc = launch_chunk(k, safe))) return rc;
 
     // The encoder wrote sizes and bounds into pinned host memory; wait for it,
     // since callers need the sizes on the host (cuszp_wrapper.cpp:520-532).
     hipError_t e = wait_stream(stream);
     if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
-    if (__atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq ||
-        __atomic_load_n(&c->host_ctl[kHostAbort], __ATOMIC_ACQUIRE) == seq) {
-        // A persistent launch's staged payload overflowed (rates near 31
-        // throughout), or a bounded wait gave up (the device was shared):
-        // encode those launches again with the schedule that needs no
-        // residency, under fresh epochs.
+    if (__atomic_load_n(&c->host_ctl[kHostAbort], __ATOMIC_ACQUIRE) == seq) {
+        // A bounded wait gave up (the device was shared): encode those
+        // launches again with the schedule that needs no residency, under
+        // fresh epochs.
         for (size_t k = 0; k < chunks.size(); ++k)
             if (redo_candidate[k] && (rc = launch_chunk(k, true))) return rc;
         e = wait_stream(stream);
@@ -585,6 +592,47 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
     for (size_t i = 0; i < batch; ++i) {
         sizes_out[i] = host_sizes[i];
         bounds_out[i] = relative ? host_bounds[i] : jobs[i].eps;
+    }
+    if (__atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq) {
+        // Jobs whose staged payload overflowed in the persistent encoder
+        // (rates near 31 throughout): those jobs again, one workgroup per tile.
+        std::vector<const void*> in;
+        std::vector<void*> out;
+        std::vector<uint64_t> cap;
+        std::vector<float> eps;
+        std::vector<size_t> where;
+        std::vector<GroupSpec> sub;
+        size_t j = 0;
+        for (size_t gi = 0; gi < specs.size(); ++gi) {
+            // the marked jobs of a group form one group of the new call
+            bool open = false;
+            for (uint32_t k = 0; k < specs[gi].jobs; ++k, ++j) {
+                if (host_redo[j] != seq) continue;
+                if (!open) {
+                    sub.push_back(specs[gi]);
+                    sub.back().jobs = 0;
+                    open = true;
+                }
+                sub.back().jobs += 1;
+                in.push_back(inputs[j]);
+                out.push_back(outputs[j]);
+                cap.push_back(capacities ? capacities[j] : ~0ull);
+                eps.push_back(jobs[j].eps);
+                where.push_back(j);
+            }
+        }
+        if (!where.empty()) {
+            std::vector<uint64_t> sz(where.size());
+            std::vector<float> eb(where.size());
+            rc = compress_groups(c, in.data(), out.data(), cap.data(), eps.data(),
+                                 where.size(), sub, stream, sz.data(), eb.data(), f32, true);
+            if (rc) return rc;
+            for (size_t k = 0; k < where.size(); ++k) {
+                sizes_out[where[k]] = sz[k];
+                bounds_out[where[k]] = eb[k];
+            }
+            c->redone += 1;
+        }
     }
     return KVSZP_OK;
 }
@@ -769,8 +817,9 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
             e = hipHostMalloc(reinterpret_cast<void**>(&c->noalloc_stage),
                               sizeof(CompressJob) * kNoAllocMaxJobs, hipHostMallocDefault);
         if (e == hipSuccess)
-            e = hipHostMalloc(&c->noalloc_results, 8ull * kNoAllocMaxJobs,
+            e = hipHostMalloc(&c->noalloc_results, 12ull * kNoAllocMaxJobs,
                               hipHostMallocCoherent);
+        if (e == hipSuccess) std::memset(c->noalloc_results, 0, 12ull * kNoAllocMaxJobs);
         if (e != hipSuccess) {
             kvszp_destroy(c);
             return hip_fail(e, "scratch setup");
@@ -812,8 +861,8 @@ int kvszp_destroy(kvszp_ctx* c) {
         (void)hipEventDestroy(r.stop);
     }
     for (hipEvent_t ev : c->spare_events) (void)hipEventDestroy(ev);
-    DevBuf* bufs[4] = {&c->tile_state, &c->tile_minmax, &c->job_minmax,
-                       &c->tables};
+    DevBuf* bufs[5] = {&c->tile_state, &c->tile_minmax, &c->job_minmax,
+                       &c->job_flags, &c->tables};
     for (DevBuf* b : bufs)
         if (b->ptr) (void)hipFree(b->ptr);
     if (c->control) (void)hipFree(c->control);
@@ -880,6 +929,10 @@ static int scratch_epoch(kvszp_ctx* c, hipStream_t stream, uint32_t* epoch) {
     if (cur >= kEpochLimit) {
         hipError_t e = launch_fill_u64(reinterpret_cast<unsigned long long*>(c->scratch),
                                        kScratchJobs / 8, stream);
+        if (e == hipSuccess)
+            e = launch_fill_u64(reinterpret_cast<unsigned long long*>(c->scratch +
+                                                                     kScratchJobFlags),
+                                kNoAllocMaxJobs / 2, stream);
         if (e != hipSuccess) return hip_fail(e, "clearing the scratch words");
         cur = 0;
     }
@@ -955,6 +1008,7 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
                            : (tiles_per_job <= c->fused_tile_limit ? kBoundFused : kBoundPrepass);
     uint32_t* host_sizes = reinterpret_cast<uint32_t*>(c->noalloc_results);
     float* host_bounds = reinterpret_cast<float*>(host_sizes + kNoAllocMaxJobs);
+    uint32_t* host_redo = host_sizes + 2 * kNoAllocMaxJobs;
     unsigned long long* words = reinterpret_cast<unsigned long long*>(c->scratch);
     if (bound_mode == kBoundPrepass) {
         MinMaxParams m;
@@ -976,6 +1030,8 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
     p.job_minmax = words + kScratchJobMinMax / 8;
     p.host_sizes = host_sizes;
     p.host_bounds = host_bounds;
+    p.host_redo = host_redo;
+    p.job_flags = reinterpret_cast<uint32_t*>(c->scratch + kScratchJobFlags);
     p.error = error_word(c);
     p.host_ctl = c->host_ctl;
     p.seq = seq;
@@ -1424,6 +1480,32 @@ int kvszp_drain_timing(kvszp_ctx* c, double* compress_ms, int* compress_count,
     if (compress_count) *compress_count = count[KVSZP_KERNEL_COMPRESS];
     if (decompress_ms) *decompress_ms = ms[KVSZP_KERNEL_DECOMPRESS];
     if (decompress_count) *decompress_count = count[KVSZP_KERNEL_DECOMPRESS];
+    return rc;
+}
+
+int kvszp_timing_durations(kvszp_ctx* c, int kind, double* ms_out, int capacity,
+                           int* count_out) {
+    if (!c || !count_out || (capacity > 0 && !ms_out))
+        return fail(KVSZP_EINVAL, "null argument");
+    if (kind != KVSZP_KERNEL_COMPRESS && kind != KVSZP_KERNEL_DECOMPRESS)
+        return fail(KVSZP_EINVAL, "unknown kernel kind %d", kind);
+    int rc = KVSZP_OK, n = 0;
+    std::vector<TimingRecord> keep;
+    for (auto& r : c->timed) {
+        if (r.kind != kind) {
+            keep.push_back(r);
+            continue;
+        }
+        float t = 0.0f;
+        hipError_t e = hipEventSynchronize(r.stop);
+        if (e == hipSuccess) e = hipEventElapsedTime(&t, r.start, r.stop);
+        if (e != hipSuccess) rc = hip_fail(e, "timing events");
+        else if (n < capacity) ms_out[n++] = t;
+        c->spare_events.push_back(r.start);
+        c->spare_events.push_back(r.stop);
+    }
+    c->timed.swap(keep);
+    *count_out = n;
     return rc;
 }
 

@@ -67,7 +67,7 @@ struct Group {
 // which tells the host that the table copy queued before it has completed.
 constexpr int kHostErrorMarker = 0;
 constexpr int kHostSeq = 1;
-constexpr int kHostOverflow = 2;  // seq of a persistent encode that must be redone
+constexpr int kHostOverflow = 2;  // seq of a launch with jobs to encode again
 constexpr int kHostAbort = 3;     // seq of an encode whose bounded waits gave up
 constexpr int kHostCtlWords = 16;
 
@@ -92,6 +92,8 @@ struct CompressParams {
     const unsigned long long* job_minmax;  // pre-pass words, two per job
     uint32_t* host_sizes;             // out (pinned host): stream bytes per job
     float* host_bounds;               // out (pinned host): absolute bound per job
+    uint32_t* host_redo;              // out (pinned host): seq = encode the job again
+    uint32_t* job_flags;              // device, one per job: epoch = job marked
     uint32_t* error;                  // device error word (kErr* bits)
     uint32_t* host_ctl;               // pinned host control words, see above
     uint32_t seq;                     // launch sequence number
@@ -185,7 +187,8 @@ constexpr size_t kScratchTileState = 0;
 constexpr size_t kScratchTileMinMax = kScratchTileState + 8ull * kNoAllocMaxTiles;
 constexpr size_t kScratchJobMinMax = kScratchTileMinMax + 8ull * kNoAllocMaxTiles;
 constexpr size_t kScratchJobs = kScratchJobMinMax + 16ull * kNoAllocMaxJobs;
-constexpr size_t kScratchAbort = kScratchJobs + sizeof(CompressJob) * kNoAllocMaxJobs;
+constexpr size_t kScratchJobFlags = kScratchJobs + sizeof(CompressJob) * kNoAllocMaxJobs;
+constexpr size_t kScratchAbort = kScratchJobFlags + 4ull * kNoAllocMaxJobs;
 constexpr size_t kScratchBytes = kScratchAbort + 256;
 
 // Device address of this device's scratch array: looked up once per device

@@ -113,16 +113,22 @@ __device__ __forceinline__ WaitBound wait_bound(unsigned long long* word, uint32
 }
 
 // One poll of a bounded wait: true when the caller must give up.
-// `deadline` is 0 before the first poll of the wait.
-__device__ __forceinline__ bool wait_gives_up(const WaitBound& b, uint64_t& deadline) {
+// `deadline` is 0 before the first poll of the wait, `spins` counts the
+// polls.  The clock is read on every poll (a scalar read, no memory
+// traffic); the launch's mark only on every 32nd: all spinning waves read
+// that one word, and reading it on every poll makes it a hot spot that slows
+// every wait of the launch.
+__device__ __forceinline__ bool wait_gives_up(const WaitBound& b, uint64_t& deadline,
+                                              uint32_t spins) {
     const uint64_t now = (uint64_t)wall_clock64();
     if (deadline == 0) deadline = now + b.ticks + 1;
-    if ((uint32_t)load_relaxed(b.word) == b.epoch) return true;
-    if (now < deadline) return false;
-    store_relaxed(b.word, (unsigned long long)b.epoch);
-    __hip_atomic_store(&b.host_ctl[kHostAbort], b.seq, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_SYSTEM);
-    return true;
+    if (now >= deadline) {
+        store_relaxed(b.word, (unsigned long long)b.epoch);
+        __hip_atomic_store(&b.host_ctl[kHostAbort], b.seq, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+        return true;
+    }
+    return (spins & 31u) == 31u && (uint32_t)load_relaxed(b.word) == b.epoch;
 }
 
 // The first workgroup of a launch records the launch's sequence number in
@@ -594,7 +600,7 @@ __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
             need = incl ? (((incl & (~incl + 1ull)) << 1) - 1ull) : win_mask;
             if ((ready & need) == need) break;
             if (timed) {
-                if (__builtin_amdgcn_readfirstlane(wait_gives_up(*bound, deadline) ? 1 : 0)) {
+                if (__builtin_amdgcn_readfirstlane(wait_gives_up(*bound, deadline, spins) ? 1 : 0)) {
                     *gave_up = true;
                     return 0;
                 }
@@ -883,7 +889,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
                 uint64_t deadline = 0;
                 for (uint32_t spins = 0; (uint32_t)(w >> 32) != p.epoch; ++spins) {
                     if (bound.word != nullptr) {
-                        if (wait_gives_up(bound, deadline)) {
+                        if (wait_gives_up(bound, deadline, spins)) {
                             s_abort = 1;
                             break;
                         }
@@ -1352,7 +1358,7 @@ __device__ __forceinline__ bool job_keys(const CompressParams& p, uint32_t first
         uint64_t deadline = 0;
         for (uint32_t spins = 0; (uint32_t)(w >> 32) != p.epoch; ++spins) {
             if (bound.word != nullptr) {
-                if (wait_gives_up(bound, deadline)) {
+                if (wait_gives_up(bound, deadline, spins)) {
                     gave_up = true;
                     break;
                 }
@@ -1741,14 +1747,23 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         // whose transpose gives words 0..15 in stream order, and for rates
         // above 15 the high fields |q| >> 15 (words 16..31), staged exactly.
         // A wave whose payload would not fit the staging words (rates far
-        // above 15 throughout) stages nothing and tells the host, which
-        // encodes the whole launch again with the one-workgroup-per-tile
-        // kernel; the rest of this launch carries on normally.
+        // above 15 throughout, e.g. a constant page under a relative bound)
+        // stages nothing and marks its job; the host encodes the marked jobs
+        // again with the one-workgroup-per-tile kernel.  Sizes, bounds and
+        // every other job of this launch come out normally.
+        // Only the first wave to mark a job writes host memory: the marks of
+        // every wave of a saturated page would be a stream of small writes
+        // across the link, most of them to one word.
         const bool overflow = (wave_bytes >> 2) + 16u > (uint32_t)kEncStageWords;
         if (overflow) {
-            if (lane == 0)
+            if (lane == 0 &&
+                __hip_atomic_exchange(&p.job_flags[cur.job], p.epoch, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) != p.epoch) {
+                __hip_atomic_store(&p.host_redo[cur.job], p.seq, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
                 __hip_atomic_store(&p.host_ctl[kHostOverflow], p.seq, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_SYSTEM);
+            }
         } else {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {

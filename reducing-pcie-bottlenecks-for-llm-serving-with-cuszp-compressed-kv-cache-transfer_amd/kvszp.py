@@ -79,6 +79,7 @@ EXPORTS = [
     ("kvszp_synchronize", _i, [_vp, _vp]),
     ("kvszp_enable_timing", _i, [_vp, _i]),
     ("kvszp_drain_timing", _i, [_vp, _vp, _vp, _vp, _vp]),
+    ("kvszp_timing_durations", _i, [_vp, _i, _vp, _i, _vp]),
     ("kvszp_reencode_count", _i, [_vp, _vp]),
     ("kvszp_last_error", ctypes.c_char_p, []),
 ]
@@ -303,6 +304,15 @@ class Context:
             offsets, sizes, bounds, batch, destinations, layer_indices,
             selected_layers, group_sizes, num_groups, prefix_count,
             source_layers, elements_per_layer, stream)
+
+    def timing_durations(self, kind: int, capacity: int = 1 << 16) -> list:
+        """Per-launch durations (ms) of the timed launches of `kind`
+        (KERNEL_COMPRESS / KERNEL_DECOMPRESS) since the last drain."""
+        buf = (ctypes.c_double * capacity)()
+        n = ctypes.c_int()
+        check(self._lib.kvszp_timing_durations(self.handle, kind, buf, capacity,
+                                               ctypes.byref(n)))
+        return [buf[i] for i in range(n.value)]
 
     def reencode_count(self) -> int:
         """Compress calls encoded again with the pre-pass schedule (a

@@ -461,3 +461,20 @@ def test_stream_capacity_covers_partial_blocks_at_rate_31(oracle):
         nb = (n + 31) // 32
         assert s.size == oracle.header_bytes(n) + 128 * nb == oracle.max_stream_bytes(n)
         assert list(s[:nb]) == [31] * nb
+
+
+def test_threaded_indexed_batch_decode_equals_page_by_page(oracle):
+    rng = np.random.default_rng(4)
+    prefix, src, epl, layers = 2, 5, 640, [4, 1, 2]
+    pages = bf16_bits(rng.standard_normal((6, prefix * src * epl)))
+    n = prefix * len(layers) * epl
+    streams, sizes, bounds = oracle.compress_batch(
+        pages, [1e-4] * 6, threads=3, layer_indices=layers, source_layers=src,
+        elements_per_layer=epl)
+    got = np.full(pages.shape, 7, dtype=np.uint16)
+    oracle.decompress_batch_indexed(streams, sizes, n, bounds, got, layers, src, epl,
+                                    threads=4)
+    for i in range(6):
+        want = np.full(pages.shape[1], 7, dtype=np.uint16)
+        oracle.decompress_indexed(streams[i], n, float(bounds[i]), want, layers, src, epl)
+        assert np.array_equal(got[i], want)
