@@ -261,7 +261,9 @@ int kvszp_pack_streams(kvszp_ctx* ctx, const void* const* payloads,
  * host-to-device copy of `packed_bytes` from the pinned slab `packed` into
  * the device buffer `staging`, then
  * kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups with stream i at
- * staging + offsets[i].  Enqueue only. */
+ * staging + offsets[i].  staging == NULL: no copy and no staging buffer;
+ * the decoder reads stream i at packed + offsets[i] across the link itself
+ * (256 workgroups, which reach the link's rate).  Enqueue only. */
 int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
     kvszp_ctx* ctx, const void* packed, uint64_t packed_bytes, void* staging,
     uint64_t staging_capacity, const uint64_t* offsets, const uint64_t* sizes,

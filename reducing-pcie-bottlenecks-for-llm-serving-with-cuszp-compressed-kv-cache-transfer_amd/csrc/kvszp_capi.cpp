@@ -63,6 +63,7 @@ struct StagingSlot {
 };
 
 constexpr int kSlots = 4;
+constexpr uint32_t kLinkDecodeGrid = 256;  // decoder workgroups reading pinned memory
 constexpr uint32_t kEpochLimit = (1u << 30) - 2u;
 constexpr uint64_t kMaxElements = 1ull << 29;      // per logical segment
 constexpr uint64_t kMaxTiles = (1ull << 32) / kThreads - 1;
@@ -646,7 +647,7 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
                       const std::vector<uint16_t*>& dst_base,
                       const std::vector<uint16_t*>& dest_table, uint64_t dpp,
                       uint64_t epd, bool aligned16, hipStream_t stream,
-                      bool f32 = false) {
+                      bool f32 = false, uint32_t grid_cap = 0) {
     int rc = use_device(c);
     if (rc) return rc;
     if (specs.empty()) return fail(KVSZP_EINVAL, "no groups");
@@ -750,7 +751,8 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         hipError_t e;
         if (c->decompress_grid != 0 && !f32) {
             p.ticket = nullptr;
-            const uint32_t grid = (uint32_t)std::min<uint64_t>(ch.tiles, c->decompress_grid);
+            uint32_t grid = (uint32_t)std::min<uint64_t>(ch.tiles, c->decompress_grid);
+            if (grid_cap) grid = std::min(grid, grid_cap);
             e = launch_decompress_persistent(p, grid, stream, timing_start(c, rec),
                                              timing_stop(c, rec));
         } else {
@@ -1369,35 +1371,44 @@ int kvszp_pack_streams(kvszp_ctx* c, const void* const* payloads, const uint64_t
     int rc = use_device(c);
     if (rc) return rc;
     // vllm_v1_compressed_offload.py:385-392: start = align8(end of the
-    // previous payload); the slab ends with the last payload.
-    std::vector<PackJob> jobs(count);
+    // previous payload); the slab ends with the last payload.  Each payload
+    // becomes pieces of at most kPackPiece bytes; the last piece of a
+    // payload zeroes the gap to the next one.
+    std::vector<PackJob> jobs;
+    jobs.reserve(count);
     uint64_t end = 0;
     for (size_t i = 0; i < count; ++i) {
         if (sizes[i] && !payloads[i]) return fail(KVSZP_EINVAL, "null payload %zu", i);
         const uint64_t start = (end + 7) & ~7ull;
-        if (i > 0) jobs[i - 1].pad = start - end;
-        jobs[i].src = static_cast<const uint8_t*>(payloads[i]);
-        jobs[i].dst_off = start;
-        jobs[i].size = sizes[i];
-        jobs[i].pad = 0;
+        if (sizes[i] && !jobs.empty())  // the gap behind the last piece written
+            jobs.back().pad = start - (jobs.back().dst_off + jobs.back().size);
+        const uint8_t* src = static_cast<const uint8_t*>(payloads[i]);
+        for (uint64_t off = 0; off < sizes[i]; off += kPackPiece)
+            jobs.push_back(PackJob{src + off, start + off,
+                                   std::min<uint64_t>(kPackPiece, sizes[i] - off), 0});
         offsets_out[i] = start;
         end = start + sizes[i];
+    }
+    if (jobs.empty()) {  // nothing but empty payloads
+        *packed_bytes_out = end;
+        return KVSZP_OK;
     }
     if (end > slab_capacity)
         return fail(KVSZP_EINVAL, "slab holds %llu bytes, the packed payloads %llu",
                     (unsigned long long)slab_capacity, (unsigned long long)end);
     *packed_bytes_out = end;
     const uint32_t seq = ++c->seq;
-    if ((rc = upload_tables(c, jobs.data(), count * sizeof(PackJob), seq, stream))) return rc;
+    if ((rc = upload_tables(c, jobs.data(), jobs.size() * sizeof(PackJob), seq, stream)))
+        return rc;
     PackParams p;
     p.jobs = reinterpret_cast<const PackJob*>(c->tables.ptr);
     p.dst = static_cast<uint8_t*>(slab);
-    p.count = (uint32_t)count;
+    p.count = (uint32_t)jobs.size();
     p.host_ctl = c->host_ctl;
     p.seq = seq;
     // Writes into pinned host memory run at the link's rate from a few dozen
     // workgroups; more only take CUs from other work.
-    const uint32_t grid = (uint32_t)std::min<size_t>(count, 128);
+    const uint32_t grid = (uint32_t)std::min<size_t>(jobs.size(), 128);
     hipError_t e = launch_pack(p, grid, stream);
     if (e != hipSuccess) return hip_fail(e, "pack launch");
     // The slab is complete when the call returns (the reference synchronizes
@@ -1416,28 +1427,61 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
     size_t source_layers, size_t elements_per_layer, kvszp_stream_t stream) {
     if (!c) return fail(KVSZP_EINVAL, "null context");
     if (batch == 0) return KVSZP_OK;
-    if (!packed || !staging || !offsets || !sizes)
+    if (!packed || !offsets || !sizes || !error_bounds || !destinations)
         return fail(KVSZP_EINVAL, "null pointer argument");
-    if (packed_bytes > staging_capacity)
+    if (staging && packed_bytes > staging_capacity)
         return fail(KVSZP_EINVAL, "staging holds %llu bytes, the slab %llu",
                     (unsigned long long)staging_capacity, (unsigned long long)packed_bytes);
+    if (num_groups == 0 || !layer_indices || !selected_layers || !group_sizes)
+        return fail(KVSZP_EINVAL, "empty group list");
+    int rc = check_fixed_config(c);
+    if (rc) return rc;
+    const uint8_t* base = static_cast<const uint8_t*>(staging ? staging : packed);
     std::vector<const void*> streams(batch);
     for (size_t i = 0; i < batch; ++i) {
         if (offsets[i] > packed_bytes || sizes[i] > packed_bytes - offsets[i])
             return fail(KVSZP_EINVAL, "payload %zu lies outside the slab", i);
-        streams[i] = static_cast<const uint8_t*>(staging) + offsets[i];
+        streams[i] = base + offsets[i];
     }
-    int rc = use_device(c);
-    if (rc) return rc;
-    // vllm_v1_compressed_offload.py:1648-1676: one host-to-device copy of the
-    // packed slab, then decode from it.
-    hipError_t e = hipMemcpyAsync(staging, packed, packed_bytes, hipMemcpyHostToDevice,
-                                  (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D packed slab)");
-    return kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups(
-        c, streams.data(), sizes, error_bounds, batch, destinations, layer_indices,
-        selected_layers, group_sizes, num_groups, prefix_count, source_layers,
-        elements_per_layer, stream);
+    std::vector<GroupSpec> specs;
+    uint64_t covered = 0;
+    for (size_t gi = 0; gi < num_groups; ++gi) {
+        if (group_sizes[gi] == 0) return fail(KVSZP_EINVAL, "group %zu is empty", gi);
+        rc = validate_layers(layer_indices[gi], selected_layers[gi], prefix_count,
+                             source_layers, elements_per_layer);
+        if (rc) return rc;
+        specs.push_back(GroupSpec{
+            (uint64_t)prefix_count * selected_layers[gi] * elements_per_layer,
+            layer_indices[gi], selected_layers[gi], source_layers, elements_per_layer,
+            (uint32_t)group_sizes[gi]});
+        covered += group_sizes[gi];
+    }
+    if (covered != batch)
+        return fail(KVSZP_EINVAL, "group sizes sum to %llu, batch is %zu",
+                    (unsigned long long)covered, batch);
+    std::vector<uint16_t*> dests(batch);
+    for (size_t i = 0; i < batch; ++i) {
+        const uintptr_t d = (uintptr_t)destinations[i];
+        if (!d || (d & 1u)) return fail(KVSZP_EINVAL, "invalid BF16 destination page %zu", i);
+        dests[i] = reinterpret_cast<uint16_t*>(d);
+    }
+    if ((rc = use_device(c))) return rc;
+    uint32_t grid_cap = 0;
+    if (staging) {
+        // vllm_v1_compressed_offload.py:1648-1676: one host-to-device copy of
+        // the packed slab, then decode from it.
+        hipError_t e = hipMemcpyAsync(staging, packed, packed_bytes, hipMemcpyHostToDevice,
+                                      (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D packed slab)");
+    } else {
+        // The decoder reads the streams across the link itself: kernel reads
+        // of pinned memory run at the link's rate from a few hundred
+        // workgroups, so a small grid does it and leaves the CUs to others.
+        grid_cap = kLinkDecodeGrid;
+    }
+    return decompress_groups(c, streams.data(), sizes, error_bounds, batch, specs,
+                             kDstIndexed, dests, {}, 0, 0, false, (hipStream_t)stream,
+                             false, grid_cap);
 }
 
 int kvszp_synchronize(kvszp_ctx* c, kvszp_stream_t stream) {

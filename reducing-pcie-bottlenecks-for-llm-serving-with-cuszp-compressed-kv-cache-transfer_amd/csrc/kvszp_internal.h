@@ -160,11 +160,14 @@ struct DecompressParams {
 // Packed publication: every payload i (src, size bytes) goes to
 // dst + dst_off, dst_off an 8-byte-aligned exclusive scan of the sizes; the
 // gap up to the next payload is zeroed.  dst may be pinned host memory.
+// Payloads are cut into pieces of at most kPackPiece bytes (one PackJob
+// each), so that any mix of payload sizes spreads over the grid.
+constexpr uint64_t kPackPiece = 64 * 1024;
 struct PackJob {
     const uint8_t* src;
     uint64_t dst_off;
     uint64_t size;
-    uint64_t pad;                     // zero bytes written after the payload
+    uint64_t pad;                     // zero bytes written after the piece
 };
 
 struct PackParams {

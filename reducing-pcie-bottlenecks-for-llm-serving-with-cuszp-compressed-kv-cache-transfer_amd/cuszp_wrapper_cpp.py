@@ -531,7 +531,8 @@ class CuSZpWrapper:
         """The packed restore (vllm_v1_compressed_offload.py:1618-1711): one
         host-to-device copy of the pinned slab `packed` into the uint8 device
         tensor `staging`, then the grouped indexed scatter of the streams at
-        `offsets`.  Enqueue only."""
+        `offsets`; staging None: the decoder reads the streams straight from
+        the pinned slab.  Enqueue only."""
         batch = len(offsets)
         if batch == 0:
             return True
@@ -539,7 +540,8 @@ class CuSZpWrapper:
                 or len(output_tensors) != batch or not layer_indices
                 or len(layer_indices) != len(group_sizes)
                 or not self._fixed_mode() or not packed.is_pinned()
-                or not self._on_device(staging) or staging.dtype != torch.uint8
+                or (staging is not None and (not self._on_device(staging)
+                                             or staging.dtype != torch.uint8))
                 or sum(int(g) for g in group_sizes) != batch):
             return False
         for idx in layer_indices:
@@ -551,8 +553,10 @@ class CuSZpWrapper:
                     or not out.is_contiguous() or out.numel() < source_elements):
                 return False
         rc = self._ctx.decompress_indexed_scatter_groups_packed(
-            packed.data_ptr(), int(packed_bytes), staging.data_ptr(),
-            staging.numel(), kvszp.u64_array([int(o) for o in offsets]),
+            packed.data_ptr(), int(packed_bytes),
+            None if staging is None else staging.data_ptr(),
+            0 if staging is None else staging.numel(),
+            kvszp.u64_array([int(o) for o in offsets]),
             kvszp.u64_array([int(s) for s in compressed_sizes]),
             kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
             kvszp.ptr_array([t.data_ptr() for t in output_tensors]),

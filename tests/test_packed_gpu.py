@@ -54,15 +54,19 @@ def test_config1_packed_store_and_restore(c1, oracle):
         assert np.array_equal(host[o:o + sizes[k]], stream), f"payload {k}"
         cursor = o + sizes[k]
     assert (host[packed:] == 0xCD).all()  # nothing past the last payload
-    # restore from the slab: one copy to the device, one grouped decode
+    # restore from the slab: one copy to the device and one grouped decode,
+    # or the decoder reading the slab across the link itself
     staging = torch.empty(packed, dtype=torch.uint8, device=DEV)
-    dest = torch.zeros_like(pages)
     _, _, _, idx, counts = req
-    assert w.decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
-        slab, packed, staging, offsets, sizes,
-        [dest[p] for p in range(pages.shape[0])] * len(counts), idx, counts, 2,
-        shape.layers, shape.elements_per_layer, bounds)
-    assert w.synchronize()
+    dests = []
+    for stage in (staging, None):
+        dest = torch.zeros_like(pages)
+        assert w.decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
+            slab, packed, stage, offsets, sizes,
+            [dest[p] for p in range(pages.shape[0])] * len(counts), idx, counts, 2,
+            shape.layers, shape.elements_per_layer, bounds)
+        assert w.synchronize()
+        dests.append(dest)
     want = np.zeros(tuple(pages.shape), dtype=np.uint16)
     k = 0
     for bound, layers in c1["groups"]:
@@ -72,7 +76,8 @@ def test_config1_packed_store_and_restore(c1, oracle):
             oracle.decompress_indexed(stream, n, float(eb), want[p], list(layers),
                                       shape.layers, shape.elements_per_layer)
             k += 1
-    assert np.array_equal(dest.view(torch.int16).cpu().numpy().view(np.uint16), want)
+    for dest in dests:
+        assert np.array_equal(dest.view(torch.int16).cpu().numpy().view(np.uint16), want)
 
 
 @pytest.mark.parametrize("where", ["pinned", "device"])
@@ -81,10 +86,12 @@ def test_pack_mixed_payloads(where):
     length and alignment, packed like the reference's slab layout."""
     g = torch.Generator().manual_seed(5)
     base = torch.randint(0, 256, (1 << 20,), generator=g, dtype=torch.uint8).to(DEV)
+    # payloads above 64 KiB are cut into pieces spread over the grid
     # (start, length): 8-, 4-, 2- and 1-byte aligned sources, odd lengths,
     # an empty payload and one that ends the slab unaligned
     spans = [(0, 4096), (4, 7), (2, 1002), (1, 33), (64, 0), (1000, 65537),
-             (8, 8), (3, 5), (4096, 131072), (6, 3)]
+             (8, 8), (3, 5), (4096, 131072), (6, 3), (16, 0), (0, 0),
+             (5, 300001), (24, 65536 * 3 + 8)]
     payloads = [base[s:s + n] for s, n in spans]
     sizes = [n for _, n in spans]
     offs, end = expected_offsets(sizes)
