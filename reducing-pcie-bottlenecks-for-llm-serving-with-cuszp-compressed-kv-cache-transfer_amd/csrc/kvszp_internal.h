@@ -9,6 +9,15 @@
 // Tiles are numbered group by group, job by job, so the tiles of a job are
 // consecutive.  A launch holds at most kMaxGroups groups (the records are
 // kernel arguments); the host splits larger calls into several launches.
+//
+// Schedules.  By default the one-workgroup-per-tile kernels take tile =
+// blockIdx.x; their only cross-workgroup waits are on tiles of lower
+// blockIdx.x, which the in-order dispatcher has started (KVSZP_TICKETS=1
+// takes tile numbers from a counter instead and turns the persistent
+// kernels off).  The persistent kernels launch the co-resident number of
+// workgroups and walk tiles b, b + G, ...: the decoder's never wait on each
+// other; the encoder's waits are bounded in time, and a launch whose wait
+// gave up is encoded again by the one-workgroup-per-tile schedule.
 #ifndef KVSZP_INTERNAL_H
 #define KVSZP_INTERNAL_H
 
