@@ -330,6 +330,138 @@ int kvo_decompress_f32(const uint8_t* stream, uint64_t stream_size, uint64_t n,
     return decode_page(stream, stream_size, n, eb, rate0_policy, &s);
 }
 
+/* ---- Lorenzo modes (plain, outlier) of the fp32 single-page API ---------
+ *
+ * CuSZpWrapper::compress/decompress hand the plain and outlier modes to
+ * upstream cuSZp (cuszp_wrapper.cpp:302-313, 922-933; the fp32 decoders at
+ * cuszp_fastpath.cu:37-59), whose sources are not vendored
+ * (reproducibility/install_cuszp.sh clones them).  What follows is this
+ * build's own specification of those modes, after the published cuSZp
+ * design (1D Lorenzo prediction inside each 32-value block, then the
+ * fixed-length block code); byte parity with upstream is unpinned.
+ *
+ * Per block: q_v = the fixed-mode quantizer's value (q_v = q_{v-1} past the
+ * end of the data), residuals d_0 = q_0, d_v = q_v - q_{v-1} (32-bit wrap).
+ * Plain codes c_v = d_v; outlier keeps o = d_0 aside and codes c_0 = 0,
+ * c_v = d_v.  With m_v = |c_v| as a 32-bit magnitude (|INT_MIN| = 2^31) the
+ * rate r is the bit length of max m_v (0..32).  Header byte: r, with bit 7
+ * set in outlier mode when o != 0.  Payload, blocks in order: o as 4 bytes
+ * (least significant first) when present, then for r > 0 the sign word and
+ * r plane words laid out exactly as in fixed mode.  Decoding: q_{-1} = o
+ * (outlier) or 0 (plain), q_v = q_{v-1} + c_v, y_v = fl(fl(q_v * eb) * 2),
+ * so both modes decode to the fixed mode's values of the same page. */
+static uint64_t encode_page_lorenzo(const float* x, uint64_t n, float eb,
+                                    int variant, int mode, uint8_t* out) {
+    const float recip = 0.5f / eb;
+    const uint64_t nb = (n + KVO_BLOCK - 1) / KVO_BLOCK;
+    const uint64_t header = kvo_header_bytes(n);
+    memset(out, 0, header);
+    uint64_t pos = header;
+    for (uint64_t b = 0; b < nb; ++b) {
+        uint32_t mag[KVO_BLOCK];
+        uint32_t sign = 0, largest = 0, outlier = 0;
+        int32_t prev = 0;
+        for (uint32_t v = 0; v < KVO_BLOCK; ++v) {
+            const uint64_t i = b * KVO_BLOCK + v;
+            const int32_t q = i < n ? kvo_quantize(x[i], recip, variant) : prev;
+            uint32_t d = (uint32_t)q - (uint32_t)prev;
+            prev = q;
+            if (mode == KVO_MODE_OUTLIER && v == 0) {
+                outlier = d;
+                d = 0;
+            }
+            uint32_t a = d;
+            if ((int32_t)d < 0) {
+                sign |= 1u << (31 - v);
+                a = 0u - d;
+            }
+            mag[v] = a;
+            if (a > largest) largest = a;
+        }
+        const int rate = kvo_bit_count(largest);
+        out[b] = (uint8_t)(rate | (outlier != 0 ? 0x80 : 0));
+        if (outlier != 0) {
+            for (int k = 0; k < 4; ++k) out[pos + k] = (uint8_t)(outlier >> (8 * k));
+            pos += 4;
+        }
+        if (rate == 0) continue;
+        put_word(out, pos, sign);
+        pos += 4;
+        for (int bit = 0; bit < rate; ++bit) {
+            uint32_t plane = 0;
+            for (uint32_t v = 0; v < KVO_BLOCK; ++v)
+                plane |= ((mag[v] >> bit) & 1u) << (31 - v);
+            put_word(out, pos, plane);
+            pos += 4;
+        }
+    }
+    return pos;
+}
+
+static int decode_page_lorenzo(const uint8_t* in, uint64_t stream_size, uint64_t n,
+                               float eb, int mode, int rate0_policy, float* out) {
+    const uint64_t nb = (n + KVO_BLOCK - 1) / KVO_BLOCK;
+    const uint64_t header = kvo_header_bytes(n);
+    if (stream_size < header) return -1;
+    uint64_t pos = header;
+    for (uint64_t b = 0; b < nb; ++b) {
+        const int h = in[b];
+        const int has_outlier = mode == KVO_MODE_OUTLIER && (h & 0x80);
+        const int rate = mode == KVO_MODE_OUTLIER ? (h & 0x7F) : h;
+        if (rate > 32) return -1;
+        if (h == 0) {
+            if (rate0_policy == KVO_RATE0_ZERO)
+                for (uint32_t v = 0; v < KVO_BLOCK && b * KVO_BLOCK + v < n; ++v)
+                    out[b * KVO_BLOCK + v] = 0.0f;
+            continue;
+        }
+        const uint64_t bytes =
+            (has_outlier ? 4u : 0u) + (rate ? 4u + 4u * (uint64_t)rate : 0u);
+        if (pos + bytes > stream_size) return -1;
+        uint32_t q = 0;
+        if (has_outlier) {
+            q = (uint32_t)in[pos] | ((uint32_t)in[pos + 1] << 8) |
+                ((uint32_t)in[pos + 2] << 16) | ((uint32_t)in[pos + 3] << 24);
+            pos += 4;
+        }
+        uint32_t sign = 0, mag[KVO_BLOCK];
+        memset(mag, 0, sizeof(mag));
+        if (rate) {
+            sign = ((uint32_t)in[pos] << 24) | ((uint32_t)in[pos + 1] << 16) |
+                   ((uint32_t)in[pos + 2] << 8) | in[pos + 3];
+            pos += 4;
+            for (int bit = 0; bit < rate; ++bit) {
+                for (uint32_t v = 0; v < KVO_BLOCK; ++v)
+                    mag[v] |= (uint32_t)((in[pos + (v >> 3)] >> (7 - (v & 7))) & 1u)
+                              << bit;
+                pos += 4;
+            }
+        }
+        for (uint32_t v = 0; v < KVO_BLOCK; ++v) {
+            const uint64_t i = b * KVO_BLOCK + v;
+            if (i >= n) break;
+            const uint32_t c = (sign & (1u << (31 - v))) ? 0u - mag[v] : mag[v];
+            q += c;
+            const float scaled = (float)(int32_t)q * eb;
+            out[i] = scaled * 2.0f;
+        }
+    }
+    return 0;
+}
+
+uint64_t kvo_compress_page_f32_mode(const float* x, uint64_t n, float eb,
+                                    int variant, int mode, uint8_t* out) {
+    if (mode == KVO_MODE_FIXED) return kvo_compress_page_f32(x, n, eb, variant, out);
+    return encode_page_lorenzo(x, n, eb, variant, mode, out);
+}
+
+int kvo_decompress_f32_mode(const uint8_t* stream, uint64_t stream_size, uint64_t n,
+                            float eb, int mode, int rate0_policy, float* out) {
+    if (mode == KVO_MODE_FIXED)
+        return kvo_decompress_f32(stream, stream_size, n, eb, rate0_policy, out);
+    return decode_page_lorenzo(stream, stream_size, n, eb, mode, rate0_policy, out);
+}
+
 /* CuSZpWrapper::compress_batch_fixed_bf16[_indexed] (cuszp_wrapper.cpp:
  * 431-681): eps_i = eps[i] > 0 ? eps[i] : default; optional relative bound;
  * size = R + payload. */

@@ -62,6 +62,18 @@ uint64_t kvo_compress_page_f32(const float* x, uint64_t n, float eb,
 int kvo_decompress_f32(const uint8_t* stream, uint64_t stream_size, uint64_t n,
                        float eb, int rate0_policy, float* out);
 
+/* Lorenzo modes of the fp32 single-page API (this build's specification of
+ * upstream cuSZp's plain and outlier modes; see kvszp_oracle.c).  `mode` is
+ * KVO_MODE_*; KVO_MODE_FIXED selects the fixed-mode functions above.  The
+ * worst-case stream is R + 136 bytes per block. */
+#define KVO_MODE_FIXED 0
+#define KVO_MODE_PLAIN 1
+#define KVO_MODE_OUTLIER 2
+uint64_t kvo_compress_page_f32_mode(const float* x, uint64_t n, float eb,
+                                    int variant, int mode, uint8_t* out);
+int kvo_decompress_f32_mode(const uint8_t* stream, uint64_t stream_size, uint64_t n,
+                            float eb, int mode, int rate0_policy, float* out);
+
 /* Decoders.  Each returns 0 on success, -1 if the stream is malformed
  * (rate > 31 or payload past stream_size). */
 int kvo_decompress_contiguous(const uint8_t* stream, uint64_t stream_size,

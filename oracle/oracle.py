@@ -26,6 +26,9 @@ QUANT_TWO_ROUNDINGS = 0
 QUANT_FUSED = 1
 RATE0_SKIP = 0
 RATE0_ZERO = 1
+MODE_FIXED = 0
+MODE_PLAIN = 1
+MODE_OUTLIER = 2
 BLOCK = 32
 REF_TILE = 32768
 
@@ -100,6 +103,14 @@ def lib() -> ctypes.CDLL:
         L.kvo_decompress_f32.restype = ctypes.c_int
         L.kvo_decompress_f32.argtypes = [
             ctypes.c_void_p, _u64, _u64, ctypes.c_float, ctypes.c_int,
+            ctypes.c_void_p]
+        L.kvo_compress_page_f32_mode.restype = _u64
+        L.kvo_compress_page_f32_mode.argtypes = [
+            ctypes.c_void_p, _u64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+            ctypes.c_void_p]
+        L.kvo_decompress_f32_mode.restype = ctypes.c_int
+        L.kvo_decompress_f32_mode.argtypes = [
+            ctypes.c_void_p, _u64, _u64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
             ctypes.c_void_p]
         L.kvo_decompress_batch_indexed.restype = ctypes.c_int
         L.kvo_decompress_batch_indexed.argtypes = [
@@ -313,6 +324,39 @@ def decompress_f32(stream, n: int, eb: float,
                                   rate0_policy, out.ctypes.data)
     if rc != 0:
         raise ValueError("malformed fixed-mode stream")
+    return out
+
+
+def max_stream_bytes_lorenzo(n: int) -> int:
+    """Worst-case plain/outlier stream: R + 136 bytes per block (a 4-byte
+    outlier, the sign word and 32 planes)."""
+    return int(lib().kvo_header_bytes(n)) + 136 * ((n + 31) // 32)
+
+
+def compress_page_f32_mode(x, eb: float, mode: int,
+                           variant: int = QUANT_TWO_ROUNDINGS) -> np.ndarray:
+    """Encode a contiguous fp32 page in MODE_FIXED, MODE_PLAIN or
+    MODE_OUTLIER (this build's specification of the last two, stated in
+    kvszp_oracle.c); returns the S stream bytes."""
+    x = _as_f32(x)
+    out = np.zeros(max(max_stream_bytes(x.size), max_stream_bytes_lorenzo(x.size)),
+                   dtype=np.uint8)
+    size = lib().kvo_compress_page_f32_mode(x.ctypes.data, x.size, eb, variant, mode,
+                                            out.ctypes.data)
+    return out[:size].copy()
+
+
+def decompress_f32_mode(stream, n: int, eb: float, mode: int,
+                        rate0_policy: int = RATE0_ZERO,
+                        out: np.ndarray | None = None) -> np.ndarray:
+    """fp32 decode of a stream of the given mode."""
+    stream = np.ascontiguousarray(np.asarray(stream, dtype=np.uint8))
+    if out is None:
+        out = np.zeros(n, dtype=np.float32)
+    rc = lib().kvo_decompress_f32_mode(stream.ctypes.data, stream.size, n, eb, mode,
+                                       rate0_policy, out.ctypes.data)
+    if rc != 0:
+        raise ValueError("malformed stream")
     return out
 
 
