@@ -196,9 +196,10 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups(
  * loads and stores.  The relative bound is the one these methods compute:
  * at::aminmax over the whole input (a NaN makes the bound NaN), range raised
  * to 1e-6f when below it, eb = eps * range (cuszp_wrapper.cpp:249-257,
- * :371-377).  Require MODE_FIXED, DIM_1D, TYPE_FLOAT; the plain/outlier modes
- * of upstream cuSZp are not provided (KVSZP_EINVAL).  Inputs and outputs are
- * contiguous fp32 arrays, 4-byte aligned. */
+ * :371-377).  The *_fixed_f32 entries require MODE_FIXED, DIM_1D,
+ * TYPE_FLOAT; kvszp_compress_f32 / kvszp_decompress_f32 /
+ * kvszp_decompress_batch_f32 below follow the context's encoding mode.
+ * Inputs and outputs are contiguous fp32 arrays, 4-byte aligned. */
 
 /* Replaces CuSZpWrapper::compress (fixed mode), cuszp_wrapper.cpp:216-325
  * (pybind11_bindings.cpp:49-64).  eps_override > 0 overrides error_bound.
@@ -238,6 +239,32 @@ int kvszp_decompress_batch_fixed_f32(kvszp_ctx* ctx,
                                      void* const* outputs,
                                      const uint64_t* num_elements,
                                      kvszp_stream_t stream);
+
+/* Replaces CuSZpWrapper::compress in every encoding mode,
+ * cuszp_wrapper.cpp:216-325 (pybind11_bindings.cpp:49-64): MODE_FIXED as
+ * kvszp_compress_fixed_f32; MODE_PLAIN and MODE_OUTLIER (the reference hands
+ * them to upstream cuSZp, :302-313) as this library's residual codes: the
+ * fixed-length block code over q_v - q_{v-1} inside each 32-value block
+ * (outlier: the block's first q kept aside as a 4-byte word).  Their byte
+ * layout is this library's own; capacity >= max(8n, R + 136 * blocks). */
+int kvszp_compress_f32(kvszp_ctx* ctx, const float* input, size_t num_elements,
+                       void* output, uint64_t capacity, float eps_override,
+                       kvszp_stream_t stream, uint64_t* size_out, float* bound_out);
+
+/* Replaces CuSZpWrapper::decompress in every encoding mode,
+ * cuszp_wrapper.cpp:870-943 (launch_cuszp_decompress_1d_f32 picks the
+ * mode's decoder, cuszp_fastpath.cu:26-59); enqueue only. */
+int kvszp_decompress_f32(kvszp_ctx* ctx, const void* compressed,
+                         uint64_t compressed_size, float* output,
+                         size_t num_elements, float error_bound,
+                         kvszp_stream_t stream);
+
+/* Replaces CuSZpWrapper::decompress_batch in every encoding mode,
+ * cuszp_wrapper.cpp:944-1033; enqueue only. */
+int kvszp_decompress_batch_f32(kvszp_ctx* ctx, const void* const* compressed,
+                               const uint64_t* sizes, const float* error_bounds,
+                               size_t batch, void* const* outputs,
+                               const uint64_t* num_elements, kvszp_stream_t stream);
 
 /* ---- packed publication and restore --------------------------------------- */
 

@@ -270,6 +270,22 @@ int check_fixed_config(const kvszp_ctx* c) {
     return KVSZP_OK;
 }
 
+// The fp32 single-page methods take every encoding mode
+// (cuszp_wrapper.cpp:268-313, 886-939) but only 1D float data.
+int check_f32_config(const kvszp_ctx* c) {
+    if (c->config.processing_dim != KVSZP_DIM_1D ||
+        c->config.data_type != KVSZP_TYPE_FLOAT)
+        return fail(KVSZP_EINVAL, "fp32 codec requires DIM_1D, TYPE_FLOAT");
+    const int m = c->config.encoding_mode;
+    if (m != KVSZP_MODE_FIXED && m != KVSZP_MODE_PLAIN && m != KVSZP_MODE_OUTLIER)
+        return fail(KVSZP_EINVAL, "unknown encoding mode %d", m);
+    return KVSZP_OK;
+}
+
+static_assert(KVSZP_MODE_FIXED == kModeFixed && KVSZP_MODE_PLAIN == kModePlain &&
+                  KVSZP_MODE_OUTLIER == kModeOutlier,
+              "kernel modes are the C ABI's");
+
 hipEvent_t take_event(kvszp_ctx* c) {
     if (!c->spare_events.empty()) {
         hipEvent_t e = c->spare_events.back();
@@ -402,14 +418,15 @@ int fill_groups(Group* groups, const std::vector<GroupSpec>& specs, const Chunk&
 // group in inputs/outputs.  `f32`: contiguous fp32 pages (the single-page
 // API, cuszp_wrapper.cpp:216-429) instead of BF16 pages.
 // `safe`: only the schedule that needs no residency (pre-pass bound, one
-// workgroup per tile).
+// workgroup per tile).  `mode` (fp32 only): kModeFixed, or the plain and
+// outlier residual codes of compress_lorenzo_kernel.
 int compress_groups(kvszp_ctx* c, const void* const* inputs,
                     void* const* outputs, const uint64_t* capacities,
                     const float* eps_overrides, size_t batch,
                     const std::vector<GroupSpec>& specs, hipStream_t stream,
                     uint64_t* sizes_out, float* bounds_out, bool f32 = false,
-                    bool safe = false) {
-    int rc = check_fixed_config(c);
+                    bool safe = false, int mode = kModeFixed) {
+    int rc = mode == kModeFixed ? check_fixed_config(c) : check_f32_config(c);
     if (rc) return rc;
     if (batch == 0) return fail(KVSZP_EINVAL, "empty batch");
     if (!inputs || !outputs || !sizes_out || !bounds_out)
@@ -431,8 +448,10 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         if (s.layers && (s.epl % 8) != 0) aligned16 = false;
         // cuszp_wrapper.cpp:449-450 asks for capacity >= estimate(4n) = 8n.
         // That does not cover the header of tiny segments (R = 1024 bytes for
-        // n < 128), so the worst-case stream R + 128 * nb is required too.
-        const uint64_t worst = header_bytes_of(s.n) + 128ull * ((s.n + 31) / 32);
+        // n < 128), so the worst-case stream R + 128 * nb is required too
+        // (R + 136 * nb in the residual modes: outlier word, sign, 32 planes).
+        const uint64_t per_block = mode == kModeFixed ? 128ull : 136ull;
+        const uint64_t worst = header_bytes_of(s.n) + per_block * ((s.n + 31) / 32);
         const uint64_t need = std::max<uint64_t>(8ull * s.n, worst);
         for (uint32_t k = 0; k < s.jobs; ++k, ++job) {
             if (job >= batch) return fail(KVSZP_EINVAL, "group sizes exceed batch");
@@ -546,6 +565,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         p.quantizer = c->quantizer;
         p.aligned16 = aligned16 ? 1 : 0;
         p.input_f32 = f32 ? 1 : 0;
+        p.mode = f32 ? mode : kModeFixed;
         const bool persistent = !safe && !f32 && bound_mode != kBoundPrepass &&
                                 c->pipelined_grid != 0 && ch.whole_blocks && aligned16 &&
                                 ch.max_tiles_per_job <= c->pipelined_grid / 2;
@@ -626,7 +646,8 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
             std::vector<uint64_t> sz(where.size());
             std::vector<float> eb(where.size());
             rc = compress_groups(c, in.data(), out.data(), cap.data(), eps.data(),
-                                 where.size(), sub, stream, sz.data(), eb.data(), f32, true);
+                                 where.size(), sub, stream, sz.data(), eb.data(), f32, true,
+                                 mode);
             if (rc) return rc;
             for (size_t k = 0; k < where.size(); ++k) {
                 sizes_out[where[k]] = sz[k];
@@ -647,7 +668,7 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
                       const std::vector<uint16_t*>& dst_base,
                       const std::vector<uint16_t*>& dest_table, uint64_t dpp,
                       uint64_t epd, bool aligned16, hipStream_t stream,
-                      bool f32 = false, uint32_t grid_cap = 0) {
+                      bool f32 = false, uint32_t grid_cap = 0, int mode = kModeFixed) {
     int rc = use_device(c);
     if (rc) return rc;
     if (specs.empty()) return fail(KVSZP_EINVAL, "no groups");
@@ -745,6 +766,7 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         p.rate0_zero = c->rate0 == KVSZP_RATE0_ZERO ? 1 : 0;
         p.aligned16 = aligned16 ? 1 : 0;
         p.output_f32 = f32 ? 1 : 0;
+        p.mode = f32 ? mode : kModeFixed;
         p.dests_per_page = dpp;
         p.elements_per_dest = epd;
         const int rec = timing_begin(c, KVSZP_KERNEL_DECOMPRESS);
@@ -1311,12 +1333,14 @@ int kvszp_compress_batch_fixed_f32(kvszp_ctx* c, const void* const* inputs,
                            specs, (hipStream_t)stream, sizes_out, bounds_out, true);
 }
 
-// Contiguous fp32 outputs, one per request, grouped by equal length.
+// Contiguous fp32 outputs, one per request, grouped by equal length;
+// `any_mode`: the context's encoding mode, else fixed mode only.
 static int decompress_f32(kvszp_ctx* c, const void* const* compressed,
                           const uint64_t* sizes, const float* error_bounds,
                           size_t batch, void* const* outputs,
-                          const uint64_t* num_elements, hipStream_t stream) {
-    int rc = check_fixed_config(c);
+                          const uint64_t* num_elements, hipStream_t stream,
+                          bool any_mode = false) {
+    int rc = any_mode ? check_f32_config(c) : check_fixed_config(c);
     if (rc) return rc;
     if (!compressed || !sizes || !error_bounds || !outputs || !num_elements)
         return fail(KVSZP_EINVAL, "null pointer argument");
@@ -1334,7 +1358,8 @@ static int decompress_f32(kvszp_ctx* c, const void* const* compressed,
         specs.back().jobs += 1;
     }
     return decompress_groups(c, compressed, sizes, error_bounds, batch, specs,
-                             kDstLinear, base, {}, 0, 0, aligned16, stream, true);
+                             kDstLinear, base, {}, 0, 0, aligned16, stream, true, 0,
+                             any_mode ? c->config.encoding_mode : kModeFixed);
 }
 
 int kvszp_decompress_fixed_f32(kvszp_ctx* c, const void* compressed,
@@ -1357,6 +1382,42 @@ int kvszp_decompress_batch_fixed_f32(kvszp_ctx* c, const void* const* compressed
     if (batch == 0) return KVSZP_OK;  // cuszp_wrapper.cpp:950
     return decompress_f32(c, compressed, sizes, error_bounds, batch, outputs,
                           num_elements, (hipStream_t)stream);
+}
+
+int kvszp_compress_f32(kvszp_ctx* c, const float* input, size_t num_elements,
+                       void* output, uint64_t capacity, float eps_override,
+                       kvszp_stream_t stream, uint64_t* size_out, float* bound_out) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    int rc = check_f32_config(c);
+    if (rc) return rc;
+    if (num_elements == 0) return fail(KVSZP_EINVAL, "empty input");
+    const void* in = input;
+    void* out = output;
+    const float eps = eps_override;  // <= 0: config.error_bound (cpp:241)
+    std::vector<GroupSpec> specs{GroupSpec{num_elements, nullptr, 0, 0, 0, 1}};
+    return compress_groups(c, &in, &out, &capacity, &eps, 1, specs,
+                           (hipStream_t)stream, size_out, bound_out, true, false,
+                           c->config.encoding_mode);
+}
+
+int kvszp_decompress_f32(kvszp_ctx* c, const void* compressed, uint64_t compressed_size,
+                         float* output, size_t num_elements, float error_bound,
+                         kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    void* out = output;
+    const uint64_t n = num_elements;
+    return decompress_f32(c, &compressed, &compressed_size, &error_bound, 1, &out, &n,
+                          (hipStream_t)stream, true);
+}
+
+int kvszp_decompress_batch_f32(kvszp_ctx* c, const void* const* compressed,
+                               const uint64_t* sizes, const float* error_bounds,
+                               size_t batch, void* const* outputs,
+                               const uint64_t* num_elements, kvszp_stream_t stream) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (batch == 0) return KVSZP_OK;  // cuszp_wrapper.cpp:950
+    return decompress_f32(c, compressed, sizes, error_bounds, batch, outputs,
+                          num_elements, (hipStream_t)stream, true);
 }
 
 int kvszp_pack_streams(kvszp_ctx* c, const void* const* payloads, const uint64_t* sizes,

@@ -38,9 +38,15 @@ constexpr uint32_t kSpinLimit = 1u << 20;           // bounded waits (~1 s)
 enum : uint32_t {
     kErrSpin = 1u,         // a bounded wait expired
     kErrLayerIndex = 2u,   // a layer index outside [0, source_layers)
-    kErrRate = 4u,         // a rate byte > 31 in a stream
+    kErrRate = 4u,         // a header byte above its mode's limit
     kErrTruncated = 8u,    // payload past the declared stream size
 };
+
+// Encoding modes of the fp32 single-page API (the values of KVSZP_MODE_*):
+// the fixed-length block code over the quantized values, or over their
+// residuals inside each 32-value block (plain), with the block's first value
+// kept aside as a 4-byte word (outlier).
+enum : int { kModeFixed = 0, kModePlain = 1, kModeOutlier = 2 };
 
 // How the relative error bound is obtained.
 enum : int {
@@ -115,6 +121,7 @@ struct CompressParams {
     int quantizer;                    // 0 two roundings, 1 fused
     int aligned16;                    // every input page is 16-byte aligned
     int input_f32;                    // pages hold fp32 values (not BF16)
+    int mode;                         // fp32 pages: kModeFixed/Plain/Outlier
     // Time-bounded waits (persistent encoder, fused bound exchange): a wait
     // longer than wait_ticks of the steady clock stores the launch's epoch
     // in *abort_word and seq in host_ctl[kHostAbort], and every wait of the
@@ -154,6 +161,7 @@ struct DecompressParams {
     int rate0_zero;                   // 1: write +0.0 for rate-0 blocks
     int aligned16;                    // every destination base 16B aligned
     int output_f32;                   // write fp32 values (kDstLinear only)
+    int mode;                         // fp32 streams: kModeFixed/Plain/Outlier
     uint64_t dests_per_page;
     uint64_t elements_per_dest;
     // Persistent decoder runs balanced by bytes moved: each tile of group

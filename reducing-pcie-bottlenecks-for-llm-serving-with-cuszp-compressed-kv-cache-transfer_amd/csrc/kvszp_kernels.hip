@@ -1009,6 +1009,189 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     }
 }
 
+// ---- Lorenzo modes (plain, outlier) of the fp32 single-page API -------------
+//
+// The reference hands these modes to upstream cuSZp (cuszp_wrapper.cpp:
+// 302-313, 922-933; decoders launched at cuszp_fastpath.cu:37-59), which is
+// not vendored.  This is the build's own specification of them, after the
+// published cuSZp design (1D Lorenzo prediction inside each 32-value block,
+// then the fixed-length block code):
+//   q_v      the fixed-mode quantizer's value; past the end of the data a
+//            block repeats its last q (residual 0)
+//   d_0 = q_0, d_v = q_v - q_{v-1}   (32-bit wrap-around)
+//   plain    codes c_v = d_v;  outlier keeps o = d_0 aside, c_0 = 0
+//   rate r   bit length of max |c_v| as a 32-bit magnitude (0..32: the
+//            magnitude of INT_MIN is 2^31)
+//   header   one byte per block: r, plus bit 7 in outlier mode when o != 0
+//   payload  per block: o (4 bytes, only when its bit is set), then for r > 0
+//            the sign word and r plane words as in fixed mode (w_32 is plane
+//            31, bit 31 of the magnitudes)
+//   decode   q_{-1} = o (outlier) or 0, q_v = q_{v-1} + c_v,
+//            y_v = fl(fl(q_v * eb) * 2)
+// Both modes decode to the fixed mode's values of the same page; byte parity
+// with upstream cuSZp is unpinned.
+
+// Residual words of one block, in place of its 32 fp32 words; returns the OR
+// of their magnitudes and the outlier word (0 in plain mode).
+template <int kQuant, int kMode>
+__device__ __forceinline__ uint32_t lorenzo_residuals(uint32_t* d, uint32_t count,
+                                                      float recip, uint32_t& outlier) {
+    int32_t prev = 0;
+    uint32_t orv = 0;
+    outlier = 0;
+#pragma unroll
+    for (int v = 0; v < kBlockElems; ++v) {
+        const int32_t q =
+            (uint32_t)v < count ? quantize<kQuant>(__uint_as_float(d[v]), recip) : prev;
+        uint32_t c = (uint32_t)q - (uint32_t)prev;
+        prev = q;
+        if (kMode == kModeOutlier && v == 0) {
+            outlier = c;
+            c = 0;
+        }
+        d[v] = c;
+        orv |= (int32_t)c < 0 ? 0u - c : c;
+    }
+    return orv;
+}
+
+__device__ __forceinline__ uint32_t residual_magnitude(uint32_t c) {
+    return (int32_t)c < 0 ? 0u - c : c;
+}
+
+// Rows of the residuals' low fields ((m << 1) | sign), high fields m >> 15
+// (bits 15..30), and the plane-31 word, in the row layout of kvszp_bits.h.
+__device__ __forceinline__ void residual_rows_lo(const uint32_t* c, uint32_t* P) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t a = c[row_lo_elem(k)], b = c[row_hi_elem(k)];
+        P[k] = field_lo(residual_magnitude(a), a >> 31) |
+               (field_lo(residual_magnitude(b), b >> 31) << 16);
+    }
+}
+
+__device__ __forceinline__ void residual_rows_hi(const uint32_t* c, uint32_t* P) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+        P[k] = field_hi(residual_magnitude(c[row_lo_elem(k)])) |
+               (field_hi(residual_magnitude(c[row_hi_elem(k)])) << 16);
+}
+
+__device__ __forceinline__ uint32_t residual_plane31(const uint32_t* c) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int v = 0; v < kBlockElems; ++v)
+        w |= (residual_magnitude(c[v]) >> 31) << (v ^ 7);
+    return w;
+}
+
+// One workgroup per tile, one block per thread, contiguous fp32 pages with
+// an absolute or pre-pass bound (the schedule of compress_kernel).
+template <int kQuant, int kMode>
+__global__ __launch_bounds__(kThreads) void compress_lorenzo_kernel(CompressParams p) {
+    __shared__ uint32_t s_tile;
+    __shared__ uint32_t s_wave[kThreads / 64];
+    __shared__ uint32_t s_prefix;
+    __shared__ uint32_t s_abort;
+    __shared__ uint8_t s_hdr[kTileBlocks];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    publish_seq(p.host_ctl, p.seq);
+    const WaitBound bound = wait_bound(p.abort_word, p.host_ctl, p.seq, p.epoch, p.wait_ticks);
+    if (tid == 0) s_abort = 0;
+    const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
+    if (t >= p.total_tiles) {
+        if (tid == 0) flag_error(p.error, p.host_ctl, kErrSpin);
+        return;
+    }
+    const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
+    const uint32_t local = t - g.first_tile;
+    const uint32_t job_in_group = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
+    const uint32_t tile = local - job_in_group * g.tiles_per_job;
+    const uint32_t job = g.first_job + job_in_group;
+    const CompressJob J = load_const(p.jobs, job);
+    const uint64_t n = g.n;
+    const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
+    const uint32_t b = tile * kTileBlocks + tid;
+    const uint64_t e0 = (uint64_t)b * kBlockElems;
+    const uint32_t count =
+        b < nb ? (uint32_t)(n - e0 < kBlockElems ? n - e0 : kBlockElems) : 0u;
+
+    uint32_t d[kBlockElems];
+    load_block_f32(reinterpret_cast<const float*>(J.in), e0, count, p.aligned16 != 0, d);
+    float eb = J.eps;
+    uint32_t bad = 0;
+    if (p.bound_mode != kBoundAbsolute) {  // pre-pass words (32-bit keys)
+        const unsigned long long wmax = p.job_minmax[2 * job];
+        const unsigned long long wmin = p.job_minmax[2 * job + 1];
+        if ((uint32_t)(wmax >> 32) != p.epoch || (uint32_t)(wmin >> 32) != p.epoch) bad = 1;
+        eb = relative_bound_f32(J.eps, 0xFFFFFFFFu - (uint32_t)wmin, (uint32_t)wmax);
+    }
+    const float recip = 0.5f / eb;  // IEEE division, as in fixed mode
+
+    uint32_t outlier;
+    const uint32_t orv = lorenzo_residuals<kQuant, kMode>(d, count, recip, outlier);
+    const uint32_t rate = orv ? 32u - (uint32_t)__builtin_clz(orv) : 0u;
+    const bool has_o = kMode == kModeOutlier && outlier != 0;
+    const uint32_t bytes = (has_o ? 4u : 0u) + (rate ? 4u + 4u * rate : 0u);
+    s_hdr[tid] = (uint8_t)(rate | (has_o ? 0x80u : 0u));
+
+    const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
+
+    const uint32_t R = g.header_bytes;
+    if (tid < kTileBlocks / 4) {
+        const uint32_t word = (uint32_t)s_hdr[4 * tid] | ((uint32_t)s_hdr[4 * tid + 1] << 8) |
+                              ((uint32_t)s_hdr[4 * tid + 2] << 16) |
+                              ((uint32_t)s_hdr[4 * tid + 3] << 24);
+        *to_global(reinterpret_cast<uint32_t*>(J.out + tile * kTileBlocks + 4 * tid)) = word;
+    }
+    const bool last_tile = tile + 1 == g.tiles_per_job;
+    if (last_tile) {
+        for (uint32_t off = (tile + 1) * kTileBlocks + 4u * tid; off < R;
+             off += 4u * kThreads)
+            *to_global(reinterpret_cast<uint32_t*>(J.out + off)) = 0u;
+    }
+    if (wave == 0) {
+        bool gave_up = false;
+        const uint32_t prefix = lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error,
+                                         p.host_ctl, &bound, &gave_up);
+        if (gave_up && lane == 0) s_abort = 1;
+        if (lane == 0) {
+            s_prefix = prefix;
+            if (last_tile)
+                __hip_atomic_store(&p.host_sizes[job], R + prefix + sc.total,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (tile == 0)
+                __hip_atomic_store(&p.host_bounds[job], eb, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+    if (bad) flag_error(p.error, p.host_ctl, kErrSpin);
+    __syncthreads();
+    if (s_abort) return;
+
+    uint32_t* dst = reinterpret_cast<uint32_t*>(J.out + R + s_prefix + sc.exclusive);
+    if (has_o) *to_global(dst) = outlier;
+    dst += has_o ? 1 : 0;
+    const uint32_t rmax = wave_max(rate);
+    if (rmax == 0) return;
+    const uint32_t count_words = rate ? rate + 1u : 0u;
+    uint32_t P[16];
+    residual_rows_lo(d, P);
+    transpose16x2(P);  // rows 0..15 = words w_0..w_15
+    store_words<16>(dst, P, count_words < 16u ? count_words : 16u,
+                    rmax < 15u ? rmax + 1u : 16u);
+    if (rmax >= 16u) {
+        residual_rows_hi(d, P);
+        transpose16x2(P);  // words w_16..w_31
+        store_words<16>(dst + 16, P, count_words > 16u ? count_words - 16u : 0u,
+                        rmax - 15u);
+        if (rate == 32u) *to_global(dst + 32) = residual_plane31(d);
+    }
+}
+
 // ---- persistent encoder ----------------------------------------------------
 //
 // For launches whose blocks are all whole, inside one layer and 16-byte
@@ -2374,6 +2557,104 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     if (err) flag_error(p.error, p.host_ctl, err);
 }
 
+// Decoder of the Lorenzo modes (specification above compress_lorenzo_kernel):
+// one workgroup per tile, one block per thread, fp32 values into contiguous
+// per-job outputs.
+template <int kMode>
+__global__ __launch_bounds__(kThreads) void decompress_lorenzo_kernel(DecompressParams p) {
+    __shared__ uint32_t s_tile;
+    __shared__ uint32_t s_wave[kThreads / 64];
+    __shared__ uint32_t s_prefix;
+    __shared__ uint32_t s_hdr[kTileBlocks / 4];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    publish_seq(p.host_ctl, p.seq);
+    const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
+    if (t >= p.total_tiles) {
+        if (tid == 0) flag_error(p.error, p.host_ctl, kErrSpin);
+        return;
+    }
+    const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
+    const uint32_t local = t - g.first_tile;
+    const uint32_t job_in_group = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
+    const uint32_t tile = local - job_in_group * g.tiles_per_job;
+    const uint32_t job = g.first_job + job_in_group;
+    const DecompressJob J = load_const(p.jobs, job);
+    const uint64_t n = g.n;
+    const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
+    const uint32_t b = tile * kTileBlocks + tid;
+    const uint64_t e0 = (uint64_t)b * kBlockElems;
+    const uint32_t count =
+        b < nb ? (uint32_t)(n - e0 < kBlockElems ? n - e0 : kBlockElems) : 0u;
+    const uint32_t R = g.header_bytes;
+
+    if (tid < kTileBlocks / 4)
+        s_hdr[tid] = *to_global(reinterpret_cast<const uint32_t*>(J.in + tile * kTileBlocks + 4 * tid));
+    __syncthreads();
+    uint32_t hdr = count ? (s_hdr[tid >> 2] >> (8 * (tid & 3))) & 0xFFu : 0u;
+    uint32_t err = 0;
+    bool has_o = kMode == kModeOutlier && (hdr & 0x80u) != 0;
+    uint32_t rate = kMode == kModeOutlier ? hdr & 0x7Fu : hdr;
+    if (rate > 32u) {
+        err |= kErrRate;
+        hdr = rate = 0;
+        has_o = false;
+    }
+    const uint32_t bytes = (has_o ? 4u : 0u) + (rate ? 4u + 4u * rate : 0u);
+    const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
+    if (wave == 0) {
+        const uint32_t pf = lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error,
+                                     p.host_ctl);
+        if (lane == 0) s_prefix = pf;
+    }
+    __syncthreads();
+    const uint64_t base = (uint64_t)R + s_prefix + sc.exclusive;
+    if (bytes && base + bytes > J.size) {
+        err |= kErrTruncated;
+        hdr = rate = 0;
+        has_o = false;
+    }
+
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(J.in + base);
+    uint32_t q = has_o ? *to_global(const_cast<uint32_t*>(src)) : 0u;
+    src += has_o ? 1 : 0;
+    const uint32_t rmax = wave_max(rate);
+    const uint32_t count_words = rate ? rate + 1u : 0u;
+    uint32_t L[16], H[16];
+    uint32_t w32 = 0;
+    load_words<16>(src, L, count_words < 16u ? count_words : 16u,
+                   rmax < 15u ? rmax + 1u : 16u);
+    transpose16x2(L);
+    if (rmax > 15u) {
+        load_words<16>(src + 16, H, count_words > 16u ? count_words - 16u : 0u, rmax - 15u);
+        transpose16x2(H);
+        if (rate == 32u) w32 = *to_global(const_cast<uint32_t*>(src + 32));
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) H[k] = 0;
+    }
+    const bool eb2_ok = J.eb >= FLT_MIN && J.eb <= FLT_MAX / 2;
+    const float eb2 = J.eb * 2.0f;
+    uint32_t out[kBlockElems];
+#pragma unroll
+    for (int v = 0; v < kBlockElems; ++v) {
+        const int k = (v & 15) ^ 7, sh = v < 16 ? 0 : 16;
+        const uint32_t lo = (L[k] >> sh) & 0xFFFFu;
+        const uint32_t m = (lo >> 1) | (((H[k] >> sh) & 0xFFFFu) << 15) |
+                           (((w32 >> (v ^ 7)) & 1u) << 31);
+        const uint32_t sg = lo & 1u;
+        q += (m ^ (0u - sg)) + sg;
+        // fl(fl(q*eb)*2) == fl(q*(2eb)) for FLT_MIN <= eb <= FLT_MAX/2
+        const float y = eb2_ok ? (float)(int32_t)q * eb2 : ((float)(int32_t)q * J.eb) * 2.0f;
+        out[v] = __float_as_uint(y);
+    }
+    if (count != 0 && (hdr != 0 || p.rate0_zero))
+        store_block_f32(reinterpret_cast<float*>(J.dst) + e0, out, count);
+    if (err) flag_error(p.error, p.host_ctl, err);
+}
+
 // ---- persistent decoder ----------------------------------------------------
 //
 // Workgroup w decodes the consecutive tiles [w*T/G, (w+1)*T/G) of the launch
@@ -2640,7 +2921,18 @@ static void launch(void (*kernel)(Args...), uint32_t grid, hipStream_t stream,
 
 hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
                            hipEvent_t start, hipEvent_t stop) {
-    if (p.input_f32) {
+    if (p.input_f32 && p.mode != kModeFixed) {
+        if (p.mode == kModePlain) {
+            if (p.quantizer)
+                launch(compress_lorenzo_kernel<1, kModePlain>, p.total_tiles, stream, start, stop, p);
+            else
+                launch(compress_lorenzo_kernel<0, kModePlain>, p.total_tiles, stream, start, stop, p);
+        } else if (p.quantizer) {
+            launch(compress_lorenzo_kernel<1, kModeOutlier>, p.total_tiles, stream, start, stop, p);
+        } else {
+            launch(compress_lorenzo_kernel<0, kModeOutlier>, p.total_tiles, stream, start, stop, p);
+        }
+    } else if (p.input_f32) {
         if (p.quantizer)
             launch(compress_kernel<1, 1>, p.total_tiles, stream, start, stop, p);
         else
@@ -2703,7 +2995,12 @@ int decompress_resident_workgroups(int device) {
 hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
                              hipEvent_t start, hipEvent_t stop) {
     if (p.output_f32) {
-        launch(decompress_kernel<kDstLinear, 1>, p.total_tiles, stream, start, stop, p);
+        if (p.mode == kModePlain)
+            launch(decompress_lorenzo_kernel<kModePlain>, p.total_tiles, stream, start, stop, p);
+        else if (p.mode == kModeOutlier)
+            launch(decompress_lorenzo_kernel<kModeOutlier>, p.total_tiles, stream, start, stop, p);
+        else
+            launch(decompress_kernel<kDstLinear, 1>, p.total_tiles, stream, start, stop, p);
         return hipGetLastError();
     }
     switch (p.dst_kind) {

@@ -219,6 +219,15 @@ class CuSZpWrapper:
                 and c.data_type == CuszpType.TYPE_FLOAT
                 and c.encoding_mode == CuszpMode.MODE_FIXED)
 
+    def _f32_1d(self) -> bool:
+        # the single-page fp32 methods take any encoding mode
+        # (cuszp_wrapper.cpp:268-313, 886-939)
+        c = self._config
+        return (c.processing_dim == CuszpDim.DIM_1D
+                and c.data_type == CuszpType.TYPE_FLOAT
+                and c.encoding_mode in (CuszpMode.MODE_FIXED, CuszpMode.MODE_PLAIN,
+                                        CuszpMode.MODE_OUTLIER))
+
     def _finish_compress(self, rc: int, batch: int, sizes, bounds, where: str):
         if rc != kvszp.OK:
             _report(where)
@@ -579,12 +588,14 @@ class CuSZpWrapper:
             return False
         return True
 
-    # ---- single-page fp32 API (fixed mode) ------------------------------
+    # ---- single-page fp32 API ------------------------------------------
     # The reference runs upstream cuSZp's fp32 kernels here
-    # (cuszp_fastpath.cu:5-64); the stream layout is the batched BF16 one
-    # (cuszp_batched_fixed.cu:52-54), so the same HIP kernels serve it with
-    # fp32 loads and stores.  The plain/outlier modes of upstream cuSZp are
-    # not provided: those calls report failure.
+    # (cuszp_fastpath.cu:5-64).  Fixed mode: the stream layout is the
+    # batched BF16 one (cuszp_batched_fixed.cu:52-54), so the same HIP
+    # kernels serve it with fp32 loads and stores.  Plain and outlier modes
+    # (upstream's cuSZp_compress/cuSZp_decompress, :302-313, 922-933): this
+    # library's residual codes (kvszp_compress_f32 in include/kvszp.h), whose
+    # streams only this library decodes.
 
     def _fp32_ok(self, t: torch.Tensor) -> bool:
         # The reference reads data_ptr() as a dense float array without
@@ -600,16 +611,18 @@ class CuSZpWrapper:
         if not input_tensor.is_cuda:
             print("Error: Input tensor must be on GPU", file=sys.stderr)
             return (False, compressed_buffer, 0, 0.0)
-        if not self._fixed_mode() or not self._fp32_ok(input_tensor):
-            print("Error: cuSZp compression failed (fp32 fixed 1D only)",
+        if not self._f32_1d() or not self._fp32_ok(input_tensor):
+            print("Error: cuSZp compression failed (fp32 1D only)",
                   file=sys.stderr)
             return (False, compressed_buffer, 0, 0.0)
         n = input_tensor.numel()
         # estimate(nbytes) = 8n, raised to the worst-case stream for tiny
-        # inputs (a 1024-byte header per 32 768 values), which 8n does not
-        # cover below 147 values.
+        # inputs (a 1024-byte header per 32 768 values, 128 bytes per block,
+        # 136 in the plain/outlier codes), which 8n does not cover below
+        # 147 (156) values.
+        per_block = 128 if self._fixed_mode() else 136
         estimated = max(self.estimate_compressed_buffer_size(4 * n),
-                        kvszp.header_bytes(n) + 128 * ((n + 31) // 32))
+                        kvszp.header_bytes(n) + per_block * ((n + 31) // 32))
         if (compressed_buffer.numel() * compressed_buffer.element_size()
                 < estimated or not self._on_device(compressed_buffer)
                 or not compressed_buffer.is_contiguous()):
@@ -617,7 +630,7 @@ class CuSZpWrapper:
                                             device=input_tensor.device)
         size = ctypes.c_uint64()
         bound = ctypes.c_float()
-        rc = self._ctx.compress_f32(
+        rc = self._ctx.compress_f32_mode(
             input_tensor.data_ptr(), n, compressed_buffer.data_ptr(),
             compressed_buffer.numel() * compressed_buffer.element_size(),
             _f32(eps_override), _stream_handle(self._device_id),
@@ -661,13 +674,13 @@ class CuSZpWrapper:
             print("Error: Both compressed buffer and output tensor must be on "
                   "GPU", file=sys.stderr)
             return False
-        if (not self._fixed_mode() or not self._fp32_ok(output_tensor)
+        if (not self._f32_1d() or not self._fp32_ok(output_tensor)
                 or not self._on_device(compressed_buffer)
                 or int(compressed_size) == 0):
-            print("Error: cuSZp decompression failed (fp32 fixed 1D only)",
+            print("Error: cuSZp decompression failed (fp32 1D only)",
                   file=sys.stderr)
             return False
-        rc = self._ctx.decompress_f32(
+        rc = self._ctx.decompress_f32_mode(
             compressed_buffer.data_ptr(), int(compressed_size),
             output_tensor.data_ptr(), output_tensor.numel(),
             _f32(actual_error_bound), _stream_handle(self._device_id))
@@ -687,8 +700,8 @@ class CuSZpWrapper:
                 or len(actual_error_bounds) != batch):
             print("Error: cuSZp batch metadata lengths differ", file=sys.stderr)
             return False
-        if not self._fixed_mode():
-            print("Error: cuSZp batch fast path requires 1D f32 fixed mode",
+        if not self._f32_1d():
+            print("Error: cuSZp batch fast path requires 1D f32",
                   file=sys.stderr)
             return False
         for comp, size, out in zip(compressed_buffers, compressed_sizes,
@@ -697,7 +710,7 @@ class CuSZpWrapper:
                     or int(size) == 0):
                 print("Error: invalid tensor in cuSZp batch", file=sys.stderr)
                 return False
-        rc = self._ctx.decompress_batch_f32(
+        rc = self._ctx.decompress_batch_f32_mode(
             kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
             kvszp.u64_array([int(s) for s in compressed_sizes]),
             kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,

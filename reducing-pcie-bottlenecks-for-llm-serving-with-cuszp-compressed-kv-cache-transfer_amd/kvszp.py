@@ -71,6 +71,12 @@ EXPORTS = [
      [_vp, _vp, ctypes.c_uint64, _vp, _sz, ctypes.c_float, _vp]),
     ("kvszp_decompress_batch_fixed_f32", _i,
      [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
+    ("kvszp_compress_f32", _i,
+     [_vp, _vp, _sz, _vp, ctypes.c_uint64, ctypes.c_float, _vp, _vp, _vp]),
+    ("kvszp_decompress_f32", _i,
+     [_vp, _vp, ctypes.c_uint64, _vp, _sz, ctypes.c_float, _vp]),
+    ("kvszp_decompress_batch_f32", _i,
+     [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
     ("kvszp_pack_streams", _i,
      [_vp, _vp, _vp, _sz, _vp, ctypes.c_uint64, _vp, _vp, _vp]),
     ("kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups_packed", _i,
@@ -285,6 +291,24 @@ class Context:
     def decompress_batch_f32(self, compressed, sizes, bounds, batch, outputs,
                              numels, stream) -> int:
         return self._lib.kvszp_decompress_batch_fixed_f32(
+            self.handle, compressed, sizes, bounds, batch, outputs, numels,
+            stream)
+
+    # The context's encoding mode (fixed, plain or outlier).
+    def compress_f32_mode(self, input_ptr, n, output_ptr, capacity, eps_override,
+                          stream, size_out, bound_out) -> int:
+        return self._lib.kvszp_compress_f32(
+            self.handle, input_ptr, n, output_ptr, capacity, eps_override,
+            stream, size_out, bound_out)
+
+    def decompress_f32_mode(self, compressed_ptr, size, output_ptr, n, eb,
+                            stream) -> int:
+        return self._lib.kvszp_decompress_f32(
+            self.handle, compressed_ptr, size, output_ptr, n, eb, stream)
+
+    def decompress_batch_f32_mode(self, compressed, sizes, bounds, batch, outputs,
+                                  numels, stream) -> int:
+        return self._lib.kvszp_decompress_batch_f32(
             self.handle, compressed, sizes, bounds, batch, outputs, numels,
             stream)
 

@@ -229,9 +229,11 @@ def test_fp32_api_rejects_what_it_cannot_serve(cpp):
     n = 4096
     x = torch.randn(n, device=DEV)
     buf = torch.empty(8 * n, dtype=torch.uint8, device=DEV)
-    plain = make(cpp, mode=cpp.MODE_PLAIN)  # upstream-only mode
-    assert plain.compress(x, buf)[0] is False
-    assert plain.decompress(buf, 1024, x, 1e-4) is False
+    plain = make(cpp, mode=cpp.MODE_PLAIN)
+    assert plain.compress_batch_fixed([x], [buf], [])[0] is False   # fixed only (cpp:339-342)
+    cfg = cpp.CompressionConfig(1e-4, True, cpp.DIM_2D, cpp.MODE_PLAIN, cpp.TYPE_FLOAT)
+    two_d = cpp.CuSZpWrapper(cfg, 0)
+    assert two_d.compress(x, buf)[0] is False                        # 1D only
     w = make(cpp)
     assert w.compress(x.to(torch.bfloat16), buf)[0] is False   # not fp32
     assert w.compress(x.cpu(), buf)[0] is False
