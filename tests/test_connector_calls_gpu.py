@@ -59,11 +59,13 @@ CALLS = {
     # :1948-1968 -- contiguous staging storage of B * N, then copied out
     "contiguous_staging": dict(method="decompress_batch_fixed_bf16", B=5,
                                N=PAGE_N),
-    # :566-758 -- the per-segment fallback: BF16 widened to fp32, padded to
-    # 36 864, single-page compress; restored by decompress (:2139-2144) or
-    # decompress_batch (:1970-1975), then .to(bfloat16)
+    # :566-758 -- the per-segment path: BF16 widened to fp32, padded to
+    # 36 864, single-page compress with the selected mode's wrapper (:726;
+    # "plain" is the connector's default mode, :498); restored by decompress
+    # (:2139-2144) or decompress_batch (:1970-1975), then .to(bfloat16)
     "fp32_segment": dict(method="compress", B=3, unpadded=EPL * 2,
-                         N=MIN_CUSZP_ELEMENTS),
+                         N=MIN_CUSZP_ELEMENTS,
+                         modes=("MODE_FIXED", "MODE_PLAIN", "MODE_OUTLIER")),
 }
 
 
@@ -269,9 +271,13 @@ def test_contiguous_staging(cpp, oracle, pages):
         assert np.array_equal(got[i], oracle.decompress_contiguous(streams[i], c["N"], bounds[i]))
 
 
-def test_fp32_segment(cpp, oracle, pages):
+@pytest.mark.parametrize("mode", CALLS["fp32_segment"]["modes"])
+def test_fp32_segment(cpp, oracle, pages, mode):
     c = CALLS["fp32_segment"]
-    w = fixed(cpp)
+    cfg = cpp.CompressionConfig(1e-4, True, cpp.CuszpDim.DIM_1D,
+                                getattr(cpp.CuszpMode, mode), cpp.CuszpType.TYPE_FLOAT)
+    w = cpp.CuSZpWrapper(cfg, 0)
+    m = {"MODE_FIXED": 0, "MODE_PLAIN": 1, "MODE_OUTLIER": 2}[mode]
     seg = pages[:c["B"]].view(c["B"], 2, LAYERS, EPL)[:, :, 9].reshape(c["B"], -1)
     srcs = [torch.nn.functional.pad(s.to(torch.float32), (0, c["N"] - c["unpadded"])).contiguous()
             for s in seg]
@@ -284,20 +290,23 @@ def test_fp32_segment(cpp, oracle, pages):
         xs = x.cpu().numpy()
         eb = oracle.relative_bound_f32(xs, 1e-4)
         assert np.float32(bound) == np.float32(eb)
-        stream = oracle.compress_page_f32(xs, eb)
+        stream = oracle.compress_page_f32_mode(xs, eb, m)
         assert size == stream.size and np.array_equal(buf[:size].cpu().numpy(), stream)
-        results.append((buf, size, bound, stream))
+        results.append((buf, size, bound, stream, oracle.compress_page_f32(xs, eb)))
     # restore one by one (:2139-2144) and as a batch (:1970-1975)
     singles = [torch.empty(c["N"], device=DEV) for _ in srcs]
-    for (buf, size, bound, _), out in zip(results, singles):
+    for (buf, size, bound, _, _), out in zip(results, singles):
         assert w.decompress(buf, size, out, bound)
     batch = [torch.empty(c["N"], device=DEV) for _ in srcs]
     assert w.decompress_batch([r[0] for r in results], [r[1] for r in results], batch,
                               [r[2] for r in results])
     assert w.synchronize()
-    for (_, _, bound, stream), a, b in zip(results, singles, batch):
-        want = oracle.decompress_f32(stream, c["N"], float(bound))
+    for (_, _, bound, stream, fixed_stream), a, b in zip(results, singles, batch):
+        want = oracle.decompress_f32_mode(stream, c["N"], float(bound), m)
         assert np.array_equal(a.cpu().numpy(), want) and np.array_equal(b.cpu().numpy(), want)
-        # the connector's .to(bfloat16) of the unpadded part
+        # the connector's .to(bfloat16) of the unpadded part: every mode
+        # decodes to the fixed mode's values, whose BF16 rounding is the BF16
+        # decoder's output
         rb = a[:c["unpadded"]].to(torch.bfloat16)
-        assert np.array_equal(u16(rb), oracle.decompress_contiguous(stream, c["N"], float(bound))[:c["unpadded"]])
+        assert np.array_equal(u16(rb), oracle.decompress_contiguous(
+            fixed_stream, c["N"], float(bound))[:c["unpadded"]])
