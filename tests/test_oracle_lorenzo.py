@@ -181,3 +181,73 @@ def test_worst_case_stream(oracle):
     s = oracle.compress_page_f32_mode(x, 0.5, OUTLIER)
     assert list(s[:3]) == [0x80 | 32] * 3
     assert s.size == oracle.max_stream_bytes_lorenzo(n) == 1024 + 136 * 3
+
+
+def _naive_lorenzo_stream(q, n, mode) -> bytes:
+    """A second, per-bit restatement of the residual codes (pure Python,
+    independent of kvszp_oracle.c): 32-bit wrap-around residuals, header
+    byte, outlier word, then the fixed mode's sign word and planes with
+    element v at bit 7 - (v & 7) of byte v >> 3."""
+    nb = (n + 31) // 32
+    header = bytearray(1024 * ((n + 32767) // 32768))
+    payload = bytearray()
+    for b in range(nb):
+        blk = [int(v) for v in q[32 * b:32 * b + 32]]
+        blk += [blk[-1]] * (32 - len(blk))
+        prev, codes = 0, []
+        for v in range(32):
+            codes.append(((blk[v] - prev + 2**31) % 2**32) - 2**31)
+            prev = blk[v]
+        o = 0
+        if mode == OUTLIER:
+            o, codes[0] = codes[0], 0
+        mags = [abs(c) for c in codes]
+        rate = max(mags).bit_length()
+        header[b] = rate | (0x80 if o else 0)
+        if o:
+            payload += (o & 0xFFFFFFFF).to_bytes(4, "little")
+        if rate == 0:
+            continue
+        words = [bytearray(4) for _ in range(rate + 1)]
+        for v in range(32):
+            bit = 1 << (7 - (v & 7))
+            if codes[v] < 0:
+                words[0][v >> 3] |= bit
+            for p in range(rate):
+                if (mags[v] >> p) & 1:
+                    words[1 + p][v >> 3] |= bit
+        for w in words:
+            payload += w
+    return bytes(header) + bytes(payload)
+
+
+@pytest.mark.parametrize("mode", [PLAIN, OUTLIER])
+@pytest.mark.parametrize("fused", [False, True])
+def test_streams_equal_naive_restatement(oracle, mode, fused):
+    """Whole streams, byte for byte, against the per-bit restatement fed by
+    the golden generator's own quantizer (tests/golden/make_golden.py)."""
+    import importlib.util
+    import os
+
+    spec = importlib.util.spec_from_file_location(
+        "make_golden", os.path.join(os.path.dirname(__file__), "golden", "make_golden.py"))
+    golden = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(golden)
+    rng = np.random.default_rng(21)
+    pages = [
+        (rng.standard_normal(1000) * 3).astype(np.float32),
+        np.cumsum(rng.standard_normal(2500) * 0.02).astype(np.float32),
+        np.where(np.arange(70) % 2 == 0, np.float32(-1.0), np.float32(3e38)).astype(np.float32),
+        np.array([0.0, -0.0, 1e-40, -7.5, 7.5, 2.5, 2.5, 2.5, -3e38], dtype=np.float32),
+    ]
+    special = (rng.standard_normal(700) * 50).astype(np.float32)
+    special[::31] = np.nan
+    special[3::37] = np.inf
+    pages.append(special)
+    for x in pages:
+        for eb in (np.float32(1e-3), np.float32(0.25), np.float32(7.0)):
+            recip = np.float32(np.float32(0.5) / eb)
+            q = golden.quantize(x, recip, fused)
+            want = _naive_lorenzo_stream(q, x.size, mode)
+            got = oracle.compress_page_f32_mode(x, float(eb), mode, 1 if fused else 0)
+            assert got.tobytes() == want, (x.size, float(eb))
