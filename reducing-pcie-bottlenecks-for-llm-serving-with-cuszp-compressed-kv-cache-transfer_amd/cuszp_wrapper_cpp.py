@@ -21,8 +21,13 @@ the sizes are on the host, decompress calls only enqueue.
 The single-page fp32 entry points (``compress``, ``compress_batch_fixed``,
 ``decompress``, ``decompress_batch``) run the same kernels with fp32 loads and
 stores in fixed mode (the reference uses upstream cuSZp's fp32 kernels, whose
-stream layout the batched BF16 codec shares); upstream's plain/outlier modes
-are not provided and report failure.
+stream layout the batched BF16 codec shares); the plain and outlier modes run
+this library's residual codes (kvszp_compress_f32 in include/kvszp.h).
+
+Lists of tensors are checked and turned into pointer arrays in one C++ pass
+by ``kvszp_torch_args`` (csrc/kvszp_torch_args.cpp, built by build.py next to
+this file), as the reference's pybind11 methods do in C++; without it the
+same checks run in Python.
 """
 
 from __future__ import annotations
@@ -31,6 +36,7 @@ import ctypes
 import enum
 import os
 import sys
+from array import array
 
 import numpy as np
 import torch
@@ -42,6 +48,60 @@ if _HERE not in sys.path:
 import kvszp  # noqa: E402  (the C ABI; raises if libkvszp.so is missing)
 
 kvszp.load()
+
+try:  # argument marshalling in C++ (host code, no device code)
+    import kvszp_torch_args as _targs  # noqa: E402
+except ImportError:
+    _targs = None
+
+_DTYPE_CODES: dict = {}
+
+
+def _describe(tensors, device: int, dtype, min_numel: int = 0, exact: bool = False,
+              contiguous: bool = True):
+    """(pointers, byte sizes) of `tensors` as packed uint64 bytes, or None
+    when any is not a tensor on CUDA device `device` of `dtype` (any dtype
+    for None), contiguous when `contiguous`, with numel == min_numel
+    (`exact`) or >= min_numel."""
+    if not isinstance(tensors, list):
+        tensors = list(tensors)
+    if _targs is not None:
+        code = -1
+        if dtype is not None:
+            code = _DTYPE_CODES.get(dtype)
+            if code is None:
+                code = _DTYPE_CODES[dtype] = _targs.dtype_code(dtype)
+        return _targs.describe(tensors, device, code, min_numel, exact, contiguous)
+    ptrs, sizes = array("Q"), array("Q")
+    for t in tensors:
+        if (not isinstance(t, torch.Tensor) or not t.is_cuda or t.get_device() != device
+                or (dtype is not None and t.dtype != dtype)
+                or (contiguous and not t.is_contiguous())):
+            return None
+        numel = t.numel()
+        if (numel != min_numel) if exact else (numel < min_numel):
+            return None
+        ptrs.append(t.data_ptr())
+        sizes.append(numel * t.element_size())
+    return ptrs.tobytes(), sizes.tobytes()
+
+
+def _u64s(packed: bytes):
+    """A C uint64 array from packed bytes (pointers or sizes)."""
+    return (ctypes.c_uint64 * (len(packed) // 8)).from_buffer_copy(packed)
+
+
+def _u64_values(values):
+    """A C uint64 array of integers (sizes, offsets)."""
+    a = array("Q", values)
+    return (ctypes.c_uint64 * len(a)).from_buffer(a), a
+
+
+def _f32_values(values):
+    """A C float array, each value rounded to the nearest float as pybind11
+    converts a Python float to C float."""
+    a = array("f", values)
+    return (ctypes.c_float * len(a)).from_buffer(a), a
 
 
 class CuszpDim(enum.IntEnum):
@@ -190,28 +250,11 @@ class CuSZpWrapper:
     def _on_device(self, t: torch.Tensor) -> bool:
         return t.is_cuda and t.get_device() == self._device_id
 
-    def _compress_inputs_ok(self, inputs, outputs, eps_overrides,
-                            min_numel: int, exact_numel: bool,
-                            capacity: int) -> bool:
-        for inp, out in zip(inputs, outputs):
-            if not (self._on_device(inp) and self._on_device(out)):
-                return False
-            if inp.dtype != torch.bfloat16 or out.dtype != torch.uint8:
-                return False
-            if not (inp.is_contiguous() and out.is_contiguous()):
-                return False
-            numel = inp.numel()
-            if (numel != min_numel) if exact_numel else (numel < min_numel):
-                return False
-            if out.numel() < capacity:
-                return False
-        return True
-
     @staticmethod
     def _eps_array(eps_overrides, batch: int):
         if not eps_overrides:
             return None
-        return kvszp.f32_array([_f32(e) for e in eps_overrides])
+        return _f32_values(eps_overrides)[0]
 
     def _fixed_mode(self) -> bool:
         c = self._config
@@ -232,8 +275,7 @@ class CuSZpWrapper:
         if rc != kvszp.OK:
             _report(where)
             return (False, [], [])
-        return (True, [int(sizes[i]) for i in range(batch)],
-                [float(bounds[i]) for i in range(batch)])
+        return (True, list(sizes), list(bounds))
 
     # ---- batched BF16 compress -----------------------------------------
 
@@ -246,16 +288,16 @@ class CuSZpWrapper:
                 or not self._fixed_mode()):
             return (False, [], [])
         n = input_tensors[0].numel()
-        if not self._compress_inputs_ok(input_tensors, compressed_buffers,
-                                        eps_overrides, n, True,
-                                        self.estimate_compressed_buffer_size(4 * n)):
+        ins = _describe(input_tensors, self._device_id, torch.bfloat16, n, exact=True)
+        outs = None if ins is None else _describe(
+            compressed_buffers, self._device_id, torch.uint8,
+            self.estimate_compressed_buffer_size(4 * n))
+        if outs is None:
             return (False, [], [])
         sizes = (ctypes.c_uint64 * batch)()
         bounds = (ctypes.c_float * batch)()
         rc = self._ctx.compress(
-            kvszp.ptr_array([t.data_ptr() for t in input_tensors]),
-            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
-            kvszp.u64_array([t.numel() for t in compressed_buffers]),
+            _u64s(ins[0]), _u64s(outs[0]), _u64s(outs[1]),
             self._eps_array(eps_overrides, batch), batch, n,
             _stream_handle(self._device_id), sizes, bounds)
         return self._finish_compress(rc, batch, sizes, bounds,
@@ -284,16 +326,16 @@ class CuSZpWrapper:
         sel = layer_indices.numel()
         source_elements = prefix_count * source_layers * elements_per_layer
         n = prefix_count * sel * elements_per_layer
-        if not self._compress_inputs_ok(input_tensors, compressed_buffers,
-                                        eps_overrides, source_elements, False,
-                                        self.estimate_compressed_buffer_size(4 * n)):
+        ins = _describe(input_tensors, self._device_id, torch.bfloat16, source_elements)
+        outs = None if ins is None else _describe(
+            compressed_buffers, self._device_id, torch.uint8,
+            self.estimate_compressed_buffer_size(4 * n))
+        if outs is None:
             return (False, [], [])
         sizes = (ctypes.c_uint64 * batch)()
         bounds = (ctypes.c_float * batch)()
         rc = self._ctx.compress_indexed(
-            kvszp.ptr_array([t.data_ptr() for t in input_tensors]),
-            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
-            kvszp.u64_array([t.numel() for t in compressed_buffers]),
+            _u64s(ins[0]), _u64s(outs[0]), _u64s(outs[1]),
             layer_indices.data_ptr(), sel, prefix_count, source_layers,
             elements_per_layer, self._eps_array(eps_overrides, batch), batch,
             _stream_handle(self._device_id), sizes, bounds)
@@ -320,23 +362,26 @@ class CuSZpWrapper:
         if sum(group_sizes) != batch:
             return (False, [], [])
         source_elements = prefix_count * source_layers * elements_per_layer
+        ins = _describe(input_tensors, self._device_id, torch.bfloat16, source_elements)
+        if ins is None:
+            return (False, [], [])
+        out_ptrs, out_caps = [], []
+        buffers = list(compressed_buffers)
         offset = 0
         for size, idx in zip(group_sizes, layer_indices):
             n = prefix_count * idx.numel() * elements_per_layer
-            if not self._compress_inputs_ok(
-                    input_tensors[offset:offset + size],
-                    compressed_buffers[offset:offset + size], None,
-                    source_elements, False,
-                    self.estimate_compressed_buffer_size(4 * n)):
+            outs = _describe(buffers[offset:offset + size], self._device_id, torch.uint8,
+                             self.estimate_compressed_buffer_size(4 * n))
+            if outs is None:
                 return (False, [], [])
+            out_ptrs.append(outs[0])
+            out_caps.append(outs[1])
             offset += size
         groups = len(group_sizes)
         sizes = (ctypes.c_uint64 * batch)()
         bounds = (ctypes.c_float * batch)()
         rc = self._ctx.compress_indexed_groups(
-            kvszp.ptr_array([t.data_ptr() for t in input_tensors]),
-            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
-            kvszp.u64_array([t.numel() for t in compressed_buffers]),
+            _u64s(ins[0]), _u64s(b"".join(out_ptrs)), _u64s(b"".join(out_caps)),
             kvszp.ptr_array([t.data_ptr() for t in layer_indices]),
             kvszp.size_array([t.numel() for t in layer_indices]),
             kvszp.size_array([int(s) for s in group_sizes]), groups,
@@ -349,9 +394,18 @@ class CuSZpWrapper:
 
     # ---- batched BF16 decompress -----------------------------------------
 
-    def _streams_ok(self, compressed_buffers, compressed_sizes) -> bool:
-        return all(self._on_device(t) and int(s) != 0
-                   for t, s in zip(compressed_buffers, compressed_sizes))
+    def _streams(self, compressed_buffers, compressed_sizes, actual_error_bounds):
+        """(stream pointers, sizes, bounds) for the C ABI, or None when a
+        stream is not on the device or a size is 0 (cuszp_wrapper.cpp:1065-
+        1077)."""
+        streams = _describe(compressed_buffers, self._device_id, None, contiguous=False)
+        if streams is None:
+            return None
+        sizes, keep_s = _u64_values(compressed_sizes)
+        if 0 in keep_s:
+            return None
+        bounds, keep_b = _f32_values(actual_error_bounds)
+        return _u64s(streams[0]), sizes, bounds, (keep_s, keep_b)
 
     def decompress_batch_fixed_bf16(self, compressed_buffers,
                                     compressed_sizes, output_tensor,
@@ -365,14 +419,15 @@ class CuSZpWrapper:
                 or num_elements_per_page == 0 or not output_tensor.is_cuda
                 or output_tensor.dtype != torch.bfloat16
                 or output_tensor.numel() < batch * num_elements_per_page
-                or not self._fixed_mode()
-                or not self._streams_ok(compressed_buffers, compressed_sizes)):
+                or not self._fixed_mode()):
+            print("Error: invalid cuSZp fixed BF16 batch metadata", file=sys.stderr)
+            return False
+        st = self._streams(compressed_buffers, compressed_sizes, actual_error_bounds)
+        if st is None:
             print("Error: invalid cuSZp fixed BF16 batch metadata", file=sys.stderr)
             return False
         rc = self._ctx.decompress(
-            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
-            kvszp.u64_array([int(s) for s in compressed_sizes]),
-            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
+            st[0], st[1], st[2], batch,
             output_tensor.data_ptr(), output_tensor.numel(),
             num_elements_per_page, _stream_handle(self._device_id))
         if rc != kvszp.OK:
@@ -395,22 +450,20 @@ class CuSZpWrapper:
                 or num_elements_per_page
                 != destinations_per_page * elements_per_destination
                 or len(output_tensors) != batch * destinations_per_page
-                or not self._fixed_mode()
-                or not self._streams_ok(compressed_buffers, compressed_sizes)):
+                or not self._fixed_mode()):
             print("Error: invalid cuSZp direct-scatter metadata", file=sys.stderr)
             return False
-        for out in output_tensors:
-            if (not out.is_cuda or out.dtype != torch.bfloat16
-                    or not out.is_contiguous()
-                    or out.numel() < elements_per_destination):
-                print("Error: invalid BF16 direct-scatter destination",
-                      file=sys.stderr)
-                return False
+        st = self._streams(compressed_buffers, compressed_sizes, actual_error_bounds)
+        if st is None:
+            print("Error: invalid cuSZp direct-scatter metadata", file=sys.stderr)
+            return False
+        outs = _describe(output_tensors, self._device_id, torch.bfloat16,
+                         elements_per_destination)
+        if outs is None:
+            print("Error: invalid BF16 direct-scatter destination", file=sys.stderr)
+            return False
         rc = self._ctx.decompress_scatter(
-            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
-            kvszp.u64_array([int(s) for s in compressed_sizes]),
-            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
-            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
+            st[0], st[1], st[2], batch, _u64s(outs[0]),
             num_elements_per_page, destinations_per_page,
             elements_per_destination, _stream_handle(self._device_id))
         if rc != kvszp.OK:
@@ -437,18 +490,13 @@ class CuSZpWrapper:
                 or not self._fixed_mode()):
             return False
         source_elements = prefix_count * source_layers * elements_per_layer
-        for comp, size, out in zip(compressed_buffers, compressed_sizes,
-                                   output_tensors):
-            if (not self._on_device(comp) or int(size) == 0
-                    or not self._on_device(out)
-                    or out.dtype != torch.bfloat16 or not out.is_contiguous()
-                    or out.numel() < source_elements):
-                return False
+        st = self._streams(compressed_buffers, compressed_sizes, actual_error_bounds)
+        outs = None if st is None else _describe(
+            output_tensors, self._device_id, torch.bfloat16, source_elements)
+        if outs is None:
+            return False
         rc = self._ctx.decompress_indexed_scatter(
-            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
-            kvszp.u64_array([int(s) for s in compressed_sizes]),
-            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
-            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
+            st[0], st[1], st[2], batch, _u64s(outs[0]),
             layer_indices.data_ptr(), layer_indices.numel(), prefix_count,
             source_layers, elements_per_layer, _stream_handle(self._device_id))
         if rc != kvszp.OK:
@@ -481,18 +529,13 @@ class CuSZpWrapper:
         if sum(int(s) for s in group_sizes) != batch:
             return False
         source_elements = prefix_count * source_layers * elements_per_layer
-        for comp, size, out in zip(compressed_buffers, compressed_sizes,
-                                   output_tensors):
-            if (not self._on_device(comp) or int(size) == 0
-                    or not self._on_device(out)
-                    or out.dtype != torch.bfloat16 or not out.is_contiguous()
-                    or out.numel() < source_elements):
-                return False
+        st = self._streams(compressed_buffers, compressed_sizes, actual_error_bounds)
+        outs = None if st is None else _describe(
+            output_tensors, self._device_id, torch.bfloat16, source_elements)
+        if outs is None:
+            return False
         rc = self._ctx.decompress_indexed_scatter_groups(
-            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
-            kvszp.u64_array([int(s) for s in compressed_sizes]),
-            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
-            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
+            st[0], st[1], st[2], batch, _u64s(outs[0]),
             kvszp.ptr_array([t.data_ptr() for t in layer_indices]),
             kvszp.size_array([t.numel() for t in layer_indices]),
             kvszp.size_array([int(s) for s in group_sizes]),
@@ -518,20 +561,18 @@ class CuSZpWrapper:
             return (False, [], 0)
         if not (slab.is_pinned() or self._on_device(slab)):
             return (False, [], 0)
-        for t in payloads:
-            if not self._on_device(t) or not t.is_contiguous():
-                return (False, [], 0)
+        src = _describe(payloads, self._device_id, None)
+        if src is None:
+            return (False, [], 0)
         offsets = (ctypes.c_uint64 * count)()
         total = ctypes.c_uint64()
         rc = self._ctx.pack(
-            kvszp.ptr_array([t.data_ptr() for t in payloads]),
-            kvszp.u64_array([t.numel() * t.element_size() for t in payloads]),
-            count, slab.data_ptr(), slab.numel(), _stream_handle(self._device_id),
+            _u64s(src[0]), _u64s(src[1]), count, slab.data_ptr(), slab.numel(), _stream_handle(self._device_id),
             offsets, ctypes.byref(total))
         if rc != kvszp.OK:
             _report("packing payloads failed")
             return (False, [], 0)
-        return (True, [int(o) for o in offsets], int(total.value))
+        return (True, list(offsets), int(total.value))
 
     def decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
             self, packed, packed_bytes, staging, offsets, compressed_sizes,
@@ -557,18 +598,18 @@ class CuSZpWrapper:
             if not self._layer_index_ok(idx, source_layers):
                 return False
         source_elements = prefix_count * source_layers * elements_per_layer
-        for out in output_tensors:
-            if (not self._on_device(out) or out.dtype != torch.bfloat16
-                    or not out.is_contiguous() or out.numel() < source_elements):
-                return False
+        outs = _describe(output_tensors, self._device_id, torch.bfloat16,
+                         source_elements)
+        if outs is None:
+            return False
+        offs, keep_o = _u64_values(offsets)
+        sizes, keep_s = _u64_values(compressed_sizes)
+        bounds, keep_b = _f32_values(actual_error_bounds)
         rc = self._ctx.decompress_indexed_scatter_groups_packed(
             packed.data_ptr(), int(packed_bytes),
             None if staging is None else staging.data_ptr(),
             0 if staging is None else staging.numel(),
-            kvszp.u64_array([int(o) for o in offsets]),
-            kvszp.u64_array([int(s) for s in compressed_sizes]),
-            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
-            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
+            offs, sizes, bounds, batch, _u64s(outs[0]),
             kvszp.ptr_array([t.data_ptr() for t in layer_indices]),
             kvszp.size_array([t.numel() for t in layer_indices]),
             kvszp.size_array([int(g) for g in group_sizes]), len(group_sizes),
@@ -649,18 +690,17 @@ class CuSZpWrapper:
                 or not self._fixed_mode()):
             return (False, [], [])
         n = input_tensors[0].numel()
-        capacity = self.estimate_compressed_buffer_size(4 * n)
-        for inp, out in zip(input_tensors, compressed_buffers):
-            if (not self._fp32_ok(inp) or inp.numel() != n
-                    or not self._on_device(out) or out.dtype != torch.uint8
-                    or not out.is_contiguous() or out.numel() < capacity):
-                return (False, [], [])
+        ins = None if n == 0 else _describe(input_tensors, self._device_id,
+                                            torch.float32, n, exact=True)
+        outs = None if ins is None else _describe(
+            compressed_buffers, self._device_id, torch.uint8,
+            self.estimate_compressed_buffer_size(4 * n))
+        if outs is None:
+            return (False, [], [])
         sizes = (ctypes.c_uint64 * batch)()
         bounds = (ctypes.c_float * batch)()
         rc = self._ctx.compress_batch_f32(
-            kvszp.ptr_array([t.data_ptr() for t in input_tensors]),
-            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
-            kvszp.u64_array([t.numel() for t in compressed_buffers]),
+            _u64s(ins[0]), _u64s(outs[0]), _u64s(outs[1]),
             self._eps_array(eps_overrides, batch), batch, n,
             _stream_handle(self._device_id), sizes, bounds)
         return self._finish_compress(rc, batch, sizes, bounds,
@@ -704,18 +744,17 @@ class CuSZpWrapper:
             print("Error: cuSZp batch fast path requires 1D f32",
                   file=sys.stderr)
             return False
-        for comp, size, out in zip(compressed_buffers, compressed_sizes,
-                                   output_tensors):
-            if (not self._on_device(comp) or not self._fp32_ok(out)
-                    or int(size) == 0):
-                print("Error: invalid tensor in cuSZp batch", file=sys.stderr)
-                return False
+        st = self._streams(compressed_buffers, compressed_sizes, actual_error_bounds)
+        outs = None if st is None else _describe(
+            output_tensors, self._device_id, torch.float32, 1)
+        if outs is None:
+            print("Error: invalid tensor in cuSZp batch", file=sys.stderr)
+            return False
+        out_bytes = array("Q")
+        out_bytes.frombytes(outs[1])
+        counts, keep_c = _u64_values(b // 4 for b in out_bytes)
         rc = self._ctx.decompress_batch_f32_mode(
-            kvszp.ptr_array([t.data_ptr() for t in compressed_buffers]),
-            kvszp.u64_array([int(s) for s in compressed_sizes]),
-            kvszp.f32_array([_f32(b) for b in actual_error_bounds]), batch,
-            kvszp.ptr_array([t.data_ptr() for t in output_tensors]),
-            kvszp.u64_array([t.numel() for t in output_tensors]),
+            st[0], st[1], st[2], batch, _u64s(outs[0]), counts,
             _stream_handle(self._device_id))
         if rc != kvszp.OK:
             _report("cuSZp batched decompression failed")
