@@ -2116,6 +2116,16 @@ __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
 
 // ---- decoder ---------------------------------------------------------------
 
+// Restored values are stored non-temporally (the `nt` policy: no lasting
+// allocation in L2 and the MALL).  The codec never reads them again, and a
+// restore writes far more than it reads (BF16 pages vs compressed streams):
+// left as dirty lines in the 256 MiB MALL, they are written back while the
+// next kernel runs and take HBM bandwidth from it (on the config-1 step the
+// following store's encoder ran 58 us instead of 53 us).
+__device__ __forceinline__ void store_streaming(g_u32x4* p, const u32x4& v) {
+    __builtin_nontemporal_store(v, p);
+}
+
 // Writes the 32 decoded BF16 values of one block (16 packed pairs).
 __device__ __forceinline__ void store_block(uint16_t* dst, const uint32_t* out,
                                             uint32_t count, bool aligned16) {
@@ -2128,7 +2138,7 @@ __device__ __forceinline__ void store_block(uint16_t* dst, const uint32_t* out,
             v.y = out[4 * i + 1];
             v.z = out[4 * i + 2];
             v.w = out[4 * i + 3];
-            p[i] = v;
+            store_streaming(&p[i], v);
         }
         return;
     }
@@ -2319,7 +2329,7 @@ __device__ __forceinline__ void store_block_f32(float* dst, const uint32_t* out,
             v.y = out[4 * i + 1];
             v.z = out[4 * i + 2];
             v.w = out[4 * i + 3];
-            p[i] = v;
+            store_streaming(&p[i], v);
         }
         return;
     }
@@ -2454,8 +2464,9 @@ __device__ __forceinline__ void store_wave_run(uint16_t* run, const uint32_t* ou
     for (int i = 0; i < 4; ++i) {
         const uint32_t b = 16u * i + ((uint32_t)lane >> 2), q = (uint32_t)lane & 3u;
         const uint32_t j = 64u * q + (b ^ (4u * q));
-        d[64 * i + lane] =
-            *reinterpret_cast<const u32x4*>(stage + (j >> 4) * kThreads + 4u * (j & 15u));
+        store_streaming(&d[64 * i + lane],
+                        *reinterpret_cast<const u32x4*>(stage + (j >> 4) * kThreads +
+                                                        4u * (j & 15u)));
     }
     __builtin_amdgcn_wave_barrier();
     __asm__ volatile("" ::: "memory");  // before the cells are reused
