@@ -2659,7 +2659,9 @@ __global__ __launch_bounds__(kThreads) void decompress_lorenzo_kernel(Decompress
         q += (m ^ (0u - sg)) + sg;
         // fl(fl(q*eb)*2) == fl(q*(2eb)) for FLT_MIN <= eb <= FLT_MAX/2
         const float y = eb2_ok ? (float)(int32_t)q * eb2 : ((float)(int32_t)q * J.eb) * 2.0f;
-        out[v] = __float_as_uint(y);
+        // A block with header byte 0 is +0.0, as a rate-0 block of the fixed
+        // code, also where eb is infinite or NaN (0 * eb would be NaN).
+        out[v] = hdr ? __float_as_uint(y) : 0u;
     }
     if (count != 0 && (hdr != 0 || p.rate0_zero))
         store_block_f32(reinterpret_cast<float*>(J.dst) + e0, out, count);

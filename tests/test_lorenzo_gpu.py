@@ -97,6 +97,10 @@ def test_smooth_and_special_pages(cpp, oracle, mode):
     special[17::61] = 1e-40
     special[:64] = 0.0
     round_trip(cpp, oracle, mode, special, 1e-3, relative=False)
+    # max - min overflows to +Inf: eb = Inf, every finite value quantizes to
+    # 0, and blocks with header byte 0 decode to +0.0 (not 0 * Inf = NaN)
+    _, _, eb, out = round_trip(cpp, oracle, mode, special, 1e-2)
+    assert np.isinf(eb) and not np.isnan(out).any()
     nan = special.copy()
     nan[123] = np.nan                       # NaN bound: every q from NaN recip
     round_trip(cpp, oracle, mode, nan, 1e-4)
