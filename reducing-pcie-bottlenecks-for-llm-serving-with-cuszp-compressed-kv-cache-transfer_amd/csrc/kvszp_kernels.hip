@@ -1846,8 +1846,10 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
             if (ex0) rate0 = rate_from_keys<kQuant>(keys0, recip);
             if (ex1) rate1 = rate_from_keys<kQuant>(keys1, recip);
         } else {
-            rate0 = rate_by_quantizing<kQuant>(X0, recip);  // absent blocks are zeros
-            rate1 = rate_by_quantizing<kQuant>(X1, recip);
+            // Only existing blocks: an absent block holds zeros, and 0 * recip
+            // is NaN (rate 1) when recip is infinite (eb below 0.5 / FLT_MAX).
+            if (ex0) rate0 = rate_by_quantizing<kQuant>(X0, recip);
+            if (ex1) rate1 = rate_by_quantizing<kQuant>(X1, recip);
         }
         const uint32_t bytes0 = rate0 ? 4u + 4u * rate0 : 0u;
         const uint32_t bytes1 = rate1 ? 4u + 4u * rate1 : 0u;

@@ -135,6 +135,28 @@ def test_special_values_match_oracle(cpp, oracle, relative):
     assert_streams(oracle, bits, n, eps, relative, bufs, sizes, bounds)
 
 
+@pytest.mark.parametrize("n", [192, 8192 + 64, 100000])
+@pytest.mark.parametrize("relative", [True, False])
+def test_bounds_that_make_recip_infinite(cpp, oracle, n, relative):
+    """eb below 0.5 / FLT_MAX (a denormal absolute bound, or a relative one
+    whose eps * range underflows) makes recip infinite: nonzero values
+    saturate and zeros quantize to -1 (0 * Inf = NaN).  Blocks past the end
+    of a page stay rate 0, so the streams match the oracle and no byte past
+    a stream is written (the canary after it stays 0xAB)."""
+    pages = rand_pages(4, n, seed=n)
+    bits = u16(pages)
+    eps = [1e-40, 1e-45, 2e-39, 1e-38] if not relative else [1e-40, 1e-45, 1e-44, 3e-39]
+    w = make(cpp, relative=relative)
+    bufs = [torch.cat([b, torch.full((4096,), 0xAB, dtype=torch.uint8, device=DEV)])
+            for b in buffers(cpp, 4, n)]
+    ok, sizes, bounds = w.compress_batch_fixed_bf16(list(pages), bufs, eps)
+    assert ok
+    assert_streams(oracle, bits, n, eps, relative, bufs, sizes, bounds)
+    for i, b in enumerate(bufs):
+        tail = b[sizes[i]:].cpu().numpy()
+        assert (tail == 0xAB).all(), (i, int(np.nonzero(tail != 0xAB)[0][0]))
+
+
 def test_eps_resolution_and_default_bound(cpp, oracle):
     n = 9000
     pages = rand_pages(3, n, seed=2)
