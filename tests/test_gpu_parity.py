@@ -577,6 +577,58 @@ def test_both_decoder_schedules_match_oracle(cpp, oracle, persistent, rate0,
         assert np.array_equal(got[i * n:(i + 1) * n], want), f"page {i}"
 
 
+@pytest.mark.parametrize("persistent", ["1", "0"])
+@pytest.mark.parametrize("target", ["contiguous", "scatter", "indexed"])
+def test_malformed_streams_every_decoder(cpp, oracle, persistent, target, monkeypatch):
+    """The checks above for every batched decoder and both schedules, with
+    the bad byte in a later tile than the first: a header byte above 31 and
+    a declared size shorter than the payload are reported at the next
+    synchronize(), and the context then decodes valid streams exactly."""
+    monkeypatch.setenv("KVSZP_PERSISTENT", persistent)
+    prefix, src, epl, idx = 2, 6, 4096, [4, 1, 3]
+    full = rand_pages(3, prefix * src * epl, seed=77)
+    layer_idx = torch.tensor(idx, dtype=torch.long, device=DEV)
+    n = prefix * len(idx) * epl                 # 24576: 3 tiles of 256 blocks
+    w = make(cpp)
+    bufs = buffers(cpp, 3, n)
+    ok, sizes, bounds = w.compress_batch_fixed_bf16_indexed(
+        list(full), bufs, layer_idx, prefix, src, epl, [1e-4] * 3)
+    assert ok
+
+    def decode(streams, stream_sizes):
+        if target == "contiguous":
+            out = torch.zeros(3 * n, dtype=torch.bfloat16, device=DEV)
+            return out, w.decompress_batch_fixed_bf16(streams, stream_sizes, out, n, bounds)
+        if target == "scatter":
+            outs = [torch.zeros(n, dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+            return outs, w.decompress_batch_fixed_bf16_scatter(
+                streams, stream_sizes, outs, n, 1, n, bounds)
+        outs = torch.zeros_like(full)
+        return outs, w.decompress_batch_fixed_bf16_indexed_scatter(
+            streams, stream_sizes, list(outs), layer_idx, prefix, src, epl, bounds)
+
+    bad = [b.clone() for b in bufs]
+    bad[1][300] = 40                            # block 300 (second tile) of page 1
+    _, ok = decode(bad, sizes)
+    assert ok                                   # enqueue only
+    assert w.synchronize() is False
+    _, ok = decode(bufs, [sizes[0], sizes[1], sizes[2] - 4])
+    assert ok
+    assert w.synchronize() is False
+    out, ok = decode(bufs, sizes)
+    assert ok and w.synchronize()
+    for i in range(3):
+        stream = bufs[i][:sizes[i]].cpu().numpy()
+        if target == "indexed":
+            want = u16(torch.zeros(prefix * src * epl, dtype=torch.bfloat16))
+            oracle.decompress_indexed(stream, n, bounds[i], want, idx, src, epl)
+            got = u16(out[i])
+        else:
+            want = oracle.decompress_contiguous(stream, n, bounds[i], 1)
+            got = u16(out)[i * n:(i + 1) * n] if target == "contiguous" else u16(out[i])
+        assert np.array_equal(got, want), f"page {i}"
+
+
 def test_indexed_groups_beyond_sixteen_groups(cpp, oracle):
     """One REL bound per Qwen2.5-1.5B layer: 28 layer groups of 8 pages in
     one compress_batch_fixed_bf16_indexed_groups call (the reference takes
