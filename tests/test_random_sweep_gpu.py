@@ -6,10 +6,11 @@ pages, pages that are only 2-byte aligned, relative and absolute bounds
 (among them bounds that make 0.5 / eb overflow or underflow, and eps that
 falls back to the configured bound: zero, negative, NaN), both quantizer
 readings and both rate-0 policies, layer maps and layer groups,
-multi-destination restores, and the fp32 API in all three modes.  Every
-stream is compared byte for byte with the oracle, every returned bound with
-the oracle's fp32 bound, every restored value bit for bit, and no byte past
-a stream may change (the buffers are filled with 0xAB first).
+multi-destination restores, packed publication and restore, and the fp32
+API in all three modes.  Every stream is compared byte for byte with the
+oracle, every returned bound with the oracle's fp32 bound, every restored
+value bit for bit, and no byte past a stream may change (the buffers are
+filled with 0xAB first).
 """
 
 from __future__ import annotations
@@ -302,3 +303,75 @@ def test_random_fp32_pages(cpp, oracle, seed):
     ref = oracle.decompress_f32_mode(want, n, float(eb), mode_id)
     got = out.cpu().numpy()
     assert np.all((got.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got) & np.isnan(ref)))
+
+
+def packed_offsets(sizes):
+    """8-byte-aligned exclusive scan of the payload sizes (the slab layout
+    of vllm_v1_compressed_offload.py:371-447) and the slab's used length."""
+    offs, end = [], 0
+    for s in sizes:
+        start = (end + 7) // 8 * 8
+        offs.append(start)
+        end = start + s
+    return offs, end
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_random_packed_store_and_restore(cpp, oracle, seed):
+    """Grouped indexed store, payloads packed into one slab (pinned host or
+    device memory) and the packed grouped restore (from a device staging
+    copy or straight from the pinned slab): slab bytes equal the streams at
+    the scan offsets with zeroed gaps, and the restored pages equal the
+    oracle's decode of every stream."""
+    rng = np.random.default_rng(6000 + seed)
+    prefix, src = 2, int(rng.integers(2, 29))
+    epl = int(rng.choice([256, 1024, 4096]))
+    order = [int(v) for v in rng.permutation(src)]
+    ngroups = int(rng.integers(1, min(src, 4) + 1))
+    cuts = sorted(int(v) for v in rng.choice(np.arange(1, src), size=ngroups - 1,
+                                             replace=False))
+    groups = [sorted(order[a:b]) for a, b in zip([0] + cuts, cuts + [src])]
+    pages_n = int(rng.integers(1, 6))
+    pages = bf16_pages(rng, pages_n, prefix * src * epl,
+                       str(rng.choice(["normal", "normal", "offset", "special", "zeros"])))
+    inputs, eps, idx, counts, ns = [], [], [], [], []
+    for layers in groups:
+        inputs += list(pages)
+        eps += [float(rng.choice([1e-3, 1e-4, 1e-5]))] * pages_n
+        idx.append(torch.tensor(layers, dtype=torch.long, device=DEV))
+        counts.append(pages_n)
+        ns.append(prefix * len(layers) * epl)
+    bufs = [b for m in ns for b in canary_buffers(oracle, pages_n, m)]
+    w = wrapper(cpp, True)
+    ok, sizes, bounds = w.compress_batch_fixed_bf16_indexed_groups(inputs, bufs, idx, counts,
+                                                                   prefix, src, epl, eps)
+    assert ok
+    streams = [bufs[k][:sizes[k]] for k in range(len(bufs))]
+    want_offs, want_end = packed_offsets(sizes)
+    on_host = bool(rng.random() < 0.7)
+    slab = torch.full((want_end + 64,), 0xCD, dtype=torch.uint8)
+    slab = slab.pin_memory() if on_host else slab.to(DEV)
+    ok, offsets, packed = w.pack_payloads(streams, slab)
+    assert ok and offsets == want_offs and packed == want_end
+    host = slab.cpu().numpy()
+    cursor = 0
+    for k, s in enumerate(streams):
+        assert not host[cursor:offsets[k]].any(), ("gap", k)
+        assert np.array_equal(host[offsets[k]:offsets[k] + sizes[k]], s.cpu().numpy()), k
+        cursor = offsets[k] + sizes[k]
+    assert (host[packed:] == 0xCD).all()
+    want = np.zeros((pages_n, prefix * src * epl), dtype=np.uint16)
+    for gi, layers in enumerate(groups):
+        for p in range(pages_n):
+            k = gi * pages_n + p
+            oracle.decompress_indexed(streams[k].cpu().numpy(), ns[gi], float(bounds[k]),
+                                      want[p], layers, src, epl)
+    if on_host:
+        staging = (torch.empty(packed, dtype=torch.uint8, device=DEV)
+                   if rng.random() < 0.5 else None)
+        dest = torch.zeros_like(pages)
+        assert w.decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
+            slab, packed, staging, offsets, sizes, list(dest) * len(groups), idx, counts,
+            prefix, src, epl, bounds)
+        assert w.synchronize()
+        assert np.array_equal(u16(dest), want)
