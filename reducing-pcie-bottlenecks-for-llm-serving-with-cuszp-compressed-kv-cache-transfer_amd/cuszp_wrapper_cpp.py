@@ -104,6 +104,12 @@ def _f32_values(values):
     return (ctypes.c_float * len(a)).from_buffer(a), a
 
 
+def _as_list(c_array, fmt: str) -> list:
+    """Python ints ('Q') or floats ('f') of a C array, through its buffer:
+    iterating the ctypes array instead costs ~50 us per 1024 values."""
+    return memoryview(c_array).cast("B").cast(fmt).tolist()
+
+
 class CuszpDim(enum.IntEnum):
     DIM_1D = kvszp.DIM_1D
     DIM_2D = kvszp.DIM_2D
@@ -275,7 +281,7 @@ class CuSZpWrapper:
         if rc != kvszp.OK:
             _report(where)
             return (False, [], [])
-        return (True, list(sizes), list(bounds))
+        return (True, _as_list(sizes, "Q"), _as_list(bounds, "f"))
 
     # ---- batched BF16 compress -----------------------------------------
 
@@ -572,7 +578,7 @@ class CuSZpWrapper:
         if rc != kvszp.OK:
             _report("packing payloads failed")
             return (False, [], 0)
-        return (True, list(offsets), int(total.value))
+        return (True, _as_list(offsets, "Q"), int(total.value))
 
     def decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
             self, packed, packed_bytes, staging, offsets, compressed_sizes,
