@@ -64,6 +64,7 @@ struct StagingSlot {
 
 constexpr int kSlots = 4;
 constexpr uint32_t kLinkDecodeGrid = 256;  // decoder workgroups reading pinned memory
+constexpr size_t kJobBalancedRuns = 1024;   // batches from this size: job-balanced decoder runs
 constexpr uint32_t kEpochLimit = (1u << 30) - 2u;
 constexpr uint64_t kMaxElements = 1ull << 29;      // per logical segment
 constexpr uint64_t kMaxTiles = (1ull << 32) / kThreads - 1;
@@ -709,13 +710,64 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         max_tiles = std::max(max_tiles, ch.tiles);
     }
 
-    // Packed table: jobs, then (kDstMulti) the destination pointers.
+    // Large single-launch batches: persistent-decoder runs balanced job by
+    // job (each job weighs its BF16 output plus its payload, spread evenly
+    // over its tiles), so that pages of very different rates (all-zero,
+    // constant, heavy-tailed) do not leave some workgroups with several
+    // times the bytes of others.  Smaller batches keep the per-group
+    // weights: their table copy stays small.
+    std::vector<uint32_t> runs;
+    const bool persistent = c->decompress_grid != 0 && !f32;
+    if (persistent && chunks.size() == 1 && batch >= kJobBalancedRuns && chunks[0].tiles > 0) {
+        uint32_t grid = (uint32_t)std::min<uint64_t>(chunks[0].tiles, c->decompress_grid);
+        if (grid_cap) grid = std::min(grid, grid_cap);
+        std::vector<uint64_t> bytes(batch);
+        std::vector<uint32_t> tiles_of(batch);
+        uint64_t total = 0;
+        size_t j = 0;
+        for (const GroupSpec& spec : specs) {
+            const uint32_t R = header_bytes_of(spec.n);
+            const uint32_t tpj = (uint32_t)((spec.n + kTileElems - 1) / kTileElems);
+            for (uint32_t k = 0; k < spec.jobs; ++k, ++j) {
+                bytes[j] = 2 * spec.n + (sizes[j] - R);
+                tiles_of[j] = tpj;
+                total += bytes[j];
+            }
+        }
+        runs.resize((size_t)grid + 1);
+        size_t jj = 0;
+        uint64_t before = 0;
+        uint64_t tile_before = 0;
+        for (uint32_t b = 0; b < grid; ++b) {
+            const uint64_t target = (uint64_t)((unsigned __int128)b * total / grid);
+            while (jj < batch && before + bytes[jj] <= target) {
+                before += bytes[jj];
+                tile_before += tiles_of[jj];
+                ++jj;
+            }
+            if (jj == batch) {
+                runs[b] = (uint32_t)chunks[0].tiles;
+            } else {
+                const uint64_t i = (uint64_t)(((unsigned __int128)(target - before) * tiles_of[jj] +
+                                               bytes[jj] - 1) / bytes[jj]);
+                runs[b] = (uint32_t)(tile_before + std::min<uint64_t>(i, tiles_of[jj]));
+            }
+        }
+        runs[grid] = (uint32_t)chunks[0].tiles;
+    }
+
+    // Packed table: jobs, then (kDstMulti) the destination pointers, then
+    // the run starts.
     const size_t jobs_bytes = (batch * sizeof(DecompressJob) + 255) & ~(size_t)255;
-    std::vector<char> table(jobs_bytes + dest_table.size() * sizeof(uint16_t*));
+    const size_t dests_bytes = dest_table.size() * sizeof(uint16_t*);
+    const size_t runs_off = (jobs_bytes + dests_bytes + 15) & ~(size_t)15;
+    std::vector<char> table(runs.empty() ? jobs_bytes + dests_bytes
+                                         : runs_off + runs.size() * sizeof(uint32_t));
     std::memcpy(table.data(), jobs.data(), batch * sizeof(DecompressJob));
     if (!dest_table.empty())
-        std::memcpy(table.data() + jobs_bytes, dest_table.data(),
-                    dest_table.size() * sizeof(uint16_t*));
+        std::memcpy(table.data() + jobs_bytes, dest_table.data(), dests_bytes);
+    if (!runs.empty())
+        std::memcpy(table.data() + runs_off, runs.data(), runs.size() * sizeof(uint32_t));
     if ((rc = ensure(c->tile_state, max_tiles * 8, true, stream))) return rc;
     const uint32_t seq = ++c->seq;
     if ((rc = upload_tables(c, table.data(), table.size(), seq, stream))) return rc;
@@ -754,6 +806,9 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         p.jobs = reinterpret_cast<const DecompressJob*>(c->tables.ptr);
         p.dests = reinterpret_cast<uint16_t* const*>(
             reinterpret_cast<char*>(c->tables.ptr) + jobs_bytes);
+        if (!runs.empty())
+            p.run_starts = reinterpret_cast<const uint32_t*>(
+                reinterpret_cast<char*>(c->tables.ptr) + runs_off);
         p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
         p.error = error_word(c);
         p.host_ctl = c->host_ctl;
@@ -775,6 +830,9 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
             p.ticket = nullptr;
             uint32_t grid = (uint32_t)std::min<uint64_t>(ch.tiles, c->decompress_grid);
             if (grid_cap) grid = std::min(grid, grid_cap);
+            if (!runs.empty() && runs.size() != (size_t)grid + 1)
+                return fail(KVSZP_EINVAL, "decoder run table for %zu workgroups, launch of %u",
+                            runs.size() - 1, grid);
             e = launch_decompress_persistent(p, grid, stream, timing_start(c, rec),
                                              timing_stop(c, rec));
         } else {

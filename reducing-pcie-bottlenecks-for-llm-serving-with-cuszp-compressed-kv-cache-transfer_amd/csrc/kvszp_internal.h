@@ -168,6 +168,9 @@ struct DecompressParams {
     // g weighs tile_weight[g] (its BF16 output plus the group's average
     // payload per tile), weight_before[g] is the weight of the tiles before
     // the group, total_weight that of all tiles; 0 = equal tile counts.
+    // run_starts (gridDim.x + 1 tile numbers, or null) overrides them with
+    // runs balanced job by job.
+    const uint32_t* run_starts;
     uint64_t total_weight;
     uint64_t weight_before[kMaxGroups];
     uint32_t tile_weight[kMaxGroups];

@@ -2736,6 +2736,7 @@ __device__ __forceinline__ uint32_t header_prefix(const uint8_t* in, uint32_t ti
 // and total_tiles at b = G, so the runs tile [0, total_tiles) exactly.
 __device__ __forceinline__ uint32_t run_start(const DecompressParams& p, uint32_t b,
                                               uint32_t G) {
+    if (p.run_starts != nullptr) return load_const(p.run_starts, b < G ? b : G);
     if (p.total_weight == 0) return (uint32_t)((uint64_t)b * p.total_tiles / G);
     if (b >= G) return p.total_tiles;
     const uint64_t target = (uint64_t)b * p.total_weight / G;

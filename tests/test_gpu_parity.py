@@ -629,6 +629,39 @@ def test_malformed_streams_every_decoder(cpp, oracle, persistent, target, monkey
         assert np.array_equal(got, want), f"page {i}"
 
 
+@pytest.mark.parametrize("rate0", [0, 1])
+def test_large_batch_of_mixed_pages(cpp, oracle, rate0):
+    """1100 requests in one call: the persistent decoder's runs are then
+    balanced job by job (each job's output plus payload bytes).  Pages of
+    very different rates side by side (all-zero, constant, heavy-tailed,
+    Gaussian) and a partial last tile per page; every restored value is
+    compared with the oracle, contiguous and single-destination scatter."""
+    batch, n = 1100, 20000                      # 3 tiles per page, the last partial
+    g = torch.Generator(device="cpu").manual_seed(99)
+    x = torch.randn(batch, n, generator=g)
+    kind = torch.randint(0, 4, (batch,), generator=g)
+    x[kind == 0] = 0.0
+    x[kind == 1] = 1.5
+    heavy = kind == 2
+    x[heavy] = x[heavy] / torch.rand(int(heavy.sum()), n, generator=g).clamp_min(1e-3)
+    pages = x.to(torch.bfloat16).to(DEV)
+    w = make(cpp, rate0=rate0)
+    bufs, sizes, bounds = _encode(cpp, w, pages, [1e-4] * batch)
+    pre = np.full(n, 0x3FE0, dtype=np.uint16)                # 1.75
+    out = torch.from_numpy(np.tile(pre, batch).view(np.int16)).view(torch.bfloat16).to(DEV)
+    assert w.decompress_batch_fixed_bf16(bufs, sizes, out, n, bounds)
+    dests = [torch.full((n,), 1.75, dtype=torch.bfloat16, device=DEV) for _ in range(batch)]
+    assert w.decompress_batch_fixed_bf16_scatter(bufs, sizes, dests, n, 1, n, bounds)
+    assert w.synchronize()
+    got = u16(out).reshape(batch, n)
+    got_s = u16(torch.stack(dests))
+    for i in range(batch):
+        want = oracle.decompress_contiguous(bufs[i][:sizes[i]].cpu().numpy(), n, bounds[i],
+                                            rate0, pre.copy())
+        assert np.array_equal(got[i], want), f"page {i} (class {int(kind[i])})"
+        assert np.array_equal(got_s[i], want), f"scatter page {i}"
+
+
 def test_indexed_groups_beyond_sixteen_groups(cpp, oracle):
     """One REL bound per Qwen2.5-1.5B layer: 28 layer groups of 8 pages in
     one compress_batch_fixed_bf16_indexed_groups call (the reference takes
