@@ -1638,10 +1638,10 @@ __device__ __forceinline__ void stage_high_words(const uint32_t* P, uint32_t cou
 //
 // Per tile: the next tile starts loading; (c) its keys; (a) wave 0 gathers
 // the job's min/max and works out the bound while wave 1 finishes the
-// look-back of the tile staged one iteration earlier; the next tile's keys
-// out; (d) the staged tile's payload out; (b) per 64-block half of each
-// wave: rows, rates, the wave scan, staging; then the tile scan, header and
-// aggregate out.
+// look-back of the tile staged one iteration earlier (one barrier hands both
+// over); the next tile's keys out; (b) rates, the wave scans, the tile scan
+// (second barrier), header and aggregate out; (d) the staged tile's payload
+// out; (e) per 64-block half of each wave: rows and staging.
 //
 // Deferred stores: a tile's payload is staged in LDS at wave-relative
 // offsets and written out one iteration later, after the tile's look-back,
@@ -1649,14 +1649,18 @@ __device__ __forceinline__ void stage_high_words(const uint32_t* P, uint32_t cou
 // not wait.  Staging needs only the wave's own offsets, so each half is
 // staged as soon as its rows exist and no more than one half's rows are held.
 //
-// Wait order with deferral (ranks increase along every workgroup's program):
-// the exchange of tile t has rank t, the look-back of t rank t + G + 1/2.
-// The look-back of t needs the aggregates of tiles x < t, published after the
-// exchange of x (rank x) and look-backs of rank <= x - G + 1/2; the exchange
-// of t needs the min/max of tiles u of t's job, published after the exchange
-// of u - G (rank u - G < t, as u < t + G/2) and look-backs of rank <=
-// u - 2G + 1/2.  Every wait depends only on waits of lower rank: no cycle
-// while all G workgroups are resident.
+// Wait order with deferral: give the iteration that holds tile t rank t.
+// Its waits are the exchange of t and the look-back of t - G, both before
+// its first barrier.  The exchange needs the min/max of the tiles u of t's
+// job, published after the first barrier of the iteration holding u - G
+// (rank u - G < t, as a job has fewer than G tiles; for u = t the prologue
+// or the previous iteration of this workgroup).  The look-back of t - G
+// needs the aggregates of tiles x < t - G, published after the second
+// barrier of iteration x (rank x < t).  Earlier iterations of the same
+// workgroup have ranks t - G, t - 2G, ...  Every wait depends only on
+// iterations of lower rank: no cycle while all G workgroups are resident.
+// The flush after the loop (the last tile's look-back) waits on lower ranks
+// too.
 //
 // Without full residency (another kernel holds CUs, or a second encoder
 // launch shares the device) a wait can depend on a workgroup that has not
@@ -1803,6 +1807,26 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
                 s_bnd[parity][1] = 0.5f / eb;  // cu:166, IEEE division
                 s_fast[parity] = fast;
             }
+        } else if (pending) {
+            // wave 1 meanwhile: the pending tile's look-back (its first read
+            // went out with the loads; its predecessors published their
+            // aggregates early in the previous iteration).  The same barrier
+            // hands the prefix over.
+            const PendingTile& q = s_pend[parity ^ 1u];
+            bool gave_up = false;
+            const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
+                                              p.epoch, p.error, p.host_ctl, true, probe,
+                                              &bound, &gave_up);
+            if (gave_up && lane == 0) s_abort = 1;
+            if (lane == 0) {
+                s_prefix[parity] = pf;
+                if (q.last)
+                    __hip_atomic_store(&p.host_sizes[q.job], q.R + pf + q.total,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (q.first)
+                    __hip_atomic_store(&p.host_bounds[q.job], q.eb, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
         }
         __syncthreads();
         if (s_abort) {
@@ -1889,32 +1913,6 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
                 *to_global(reinterpret_cast<uint32_t*>(job_of(p, cur).out + off)) = 0u;
         }
         if (wave == 0) lookback_publish(p.tile_state, cur.t, cur.tile, total, p.epoch);
-
-        // The pending tile's look-back (wave 1; its first read went out with
-        // the loads, and its predecessors published their aggregates early
-        // in the previous iteration); one barrier hands the prefix over.
-        if (wave == 1 && pending) {
-            const PendingTile& q = s_pend[parity ^ 1u];
-            bool gave_up = false;
-            const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                              p.epoch, p.error, p.host_ctl, true, probe,
-                                              &bound, &gave_up);
-            if (gave_up && lane == 0) s_abort = 1;
-            if (lane == 0) {
-                s_prefix[parity] = pf;
-                if (q.last)
-                    __hip_atomic_store(&p.host_sizes[q.job], q.R + pf + q.total,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                if (q.first)
-                    __hip_atomic_store(&p.host_bounds[q.job], q.eb, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_SYSTEM);
-            }
-        }
-        __syncthreads();
-        if (s_abort) {
-            aborted = true;
-            return false;
-        }
 
         // d. the pending tile's payload out (frees the staging words)
         if (pending) {
