@@ -778,6 +778,12 @@ def main() -> int:
         "decompress_kernel": dec,
         "compress_hbm_frac": round(enc_hbm / HBM_PEAK_GBPS, 4),
         "decompress_hbm_frac": round(dec_hbm / HBM_PEAK_GBPS, 4),
+        # the same launches on the uncompressed basis (2N bytes only); the
+        # algorithmic-traffic fractions above are larger by 1 + S / 2N
+        "compress_bf16_frac": round(
+            w.bf16_bytes / (enc["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "decompress_bf16_frac": round(
+            w.bf16_bytes / (dec["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
         "mall_warm": {"compress_kernel": warm["compress"],
                       "decompress_kernel": warm["decompress"],
                       "ms_per_step": round(warm["ms_per_step"], 4)},
