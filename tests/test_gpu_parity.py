@@ -75,8 +75,11 @@ def assert_streams(oracle, pages_bits, n, eps, relative, bufs, sizes, bounds,
 
 # ---- compress: contiguous pages ----------------------------------------------
 
+# 196608 and 204800 elements: jobs of 24 and 25 tiles, the longest that the
+# persistent encoder runs with the look-back beside the bound exchange and
+# the shortest that it runs with the look-back after the tile scan
 @pytest.mark.parametrize("n", [32, 33, 1000, 8192, 8193, 32768, 36864, 100003,
-                               229376])
+                               196608, 204800, 229376])
 @pytest.mark.parametrize("relative", [True, False])
 def test_compress_bytes_match_oracle(cpp, oracle, n, relative):
     batch = 3
