@@ -92,9 +92,12 @@ def test_compress_bytes_match_oracle(cpp, oracle, n, relative):
     assert_streams(oracle, u16(pages), n, eps, relative, bufs, sizes, bounds)
 
 
+# 40000 and 229376 elements: jobs of 5 and 28 tiles, which the persistent
+# encoder runs with the look-back beside the bound exchange and after the
+# tile scan respectively
+@pytest.mark.parametrize("n", [40000, 229376])
 @pytest.mark.parametrize("quantizer", [0, 1])
-def test_quantizer_variants_match_oracle(cpp, oracle, quantizer):
-    n = 40000
+def test_quantizer_variants_match_oracle(cpp, oracle, quantizer, n):
     pages = rand_pages(2, n, seed=5)
     const = torch.full((n,), 1.3125, dtype=torch.bfloat16, device=DEV)
     pages = torch.stack([pages[0], pages[1], const])
