@@ -55,6 +55,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import gc
 import hashlib
 import json
 import os
@@ -357,16 +358,34 @@ def kernel_stats(ms: list) -> dict:
 def timed_steps(w: Workload, steps: int, sets: int) -> dict:
     """K steps over `sets` buffer sets: wall time, then the encoder's and the
     decoder's per-launch durations (each from its own pass of K steps; an
-    event pair costs a little GPU time, so only one kind is timed at once)."""
+    event pair costs a little GPU time, so only one kind is timed at once).
+
+    Each step's own wall time is kept too (from the end of the step before,
+    so the per-step times add up to the whole pass): the store blocks until
+    its sizes are on the host, and the restore is enqueued behind it, so a
+    step ends with its restore still queued and the next step's store waits
+    for it."""
     torch, k = w.torch, w.k
     torch.cuda.synchronize()
     w.ctx.enable_timing(0)
-    t0 = time.perf_counter()
+    marks = [time.perf_counter()]
     for i in range(steps):
         w.step(i % sets)
+        marks.append(time.perf_counter())
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    out = {"ms_per_step": wall / steps * 1e3}
+    end = time.perf_counter()
+    wall = end - marks[0]
+    per = [(b - a) * 1e3 for a, b in zip(marks, marks[1:])]
+    if per:
+        per[-1] += (end - marks[-1]) * 1e3  # the last restore's drain
+    out = {"ms_per_step": wall / steps * 1e3,
+           "step_ms": {"mean": round(statistics.fmean(per), 4) if per else 0.0,
+                       "median": round(statistics.median(per), 4) if per else 0.0,
+                       "min": round(min(per), 4) if per else 0.0,
+                       "max": round(max(per), 4) if per else 0.0,
+                       "first": round(per[0], 4) if per else 0.0}}
+    if os.environ.get("KVSZP_BENCH_STEP_LOG"):
+        log("step ms: " + " ".join(f"{x:.4f}" for x in per))
     for kind, key in ((k.KERNEL_COMPRESS, "compress"), (k.KERNEL_DECOMPRESS, "decompress")):
         w.ctx.timing_durations(kind)
         w.ctx.enable_timing(1 << kind)
@@ -724,6 +743,18 @@ def main() -> int:
     for i in range(max(1, warmup)):
         w.step(i % sets)
     torch.cuda.synchronize()
+    # The timed passes follow the warm-up directly.  Python's cyclic garbage
+    # collector stays off while they run (a full collection in a process
+    # holding torch takes milliseconds, and would land inside one step).
+    gc.collect()
+    gc.disable()
+    try:
+        cold = timed_steps(w, steps, sets)
+        warm = timed_steps(w, steps, 1) if sets > 1 else cold
+    finally:
+        gc.enable()
+    # Every step writes the same restored pages, so the round trip of the
+    # timed steps is checked afterwards.
     check = w.verify()
     log(f"round trip check: {check}")
     if not check["ok"]:
@@ -731,9 +762,6 @@ def main() -> int:
         return 1
     s_bytes = w.stream_bytes(0)
     ratio = w.bf16_bytes / s_bytes
-
-    cold = timed_steps(w, steps, sets)
-    warm = timed_steps(w, steps, 1) if sets > 1 else cold
     step_ms = cold["ms_per_step"]
     enc, dec = cold["compress"], cold["decompress"]
     enc_launch_bytes = (w.bf16_bytes + s_bytes) / max(1, enc["launches_per_step"])
@@ -755,6 +783,7 @@ def main() -> int:
         "steps": steps,
         "warmup": warmup,
         "ms_per_step": round(step_ms, 4),
+        "step_ms": cold["step_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

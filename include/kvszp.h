@@ -300,9 +300,11 @@ int kvszp_decompress_batch_fixed_bf16_indexed_scatter_groups_packed(
     size_t source_layers, size_t elements_per_layer, kvszp_stream_t stream);
 
 /* Waits for `stream` and reports any error a kernel of this context flagged
- * since the last check (decompress calls only enqueue, so their device-side
- * errors surface here or at the next compress call).  No reference
- * counterpart: the reference's decoders have no device-side checks. */
+ * since the last check.  Decompress calls only enqueue, so their
+ * device-side errors (malformed stream, layer index out of range) surface
+ * here; compress calls report only the errors of their own launches.  No
+ * reference counterpart: the reference's decoders have no device-side
+ * checks. */
 int kvszp_synchronize(kvszp_ctx* ctx, kvszp_stream_t stream);
 
 /* Kernel timing.  For the kernel kinds in `kinds` (a mask of KVSZP_TIME_*;
@@ -338,6 +340,15 @@ int kvszp_timing_durations(kvszp_ctx* ctx, int kind, double* ms_out,
  * 200 us) or the persistent encoder's staging overflowed.  No reference
  * counterpart: the reference's kernels assume the launch runs alone. */
 int kvszp_reencode_count(const kvszp_ctx* ctx, uint64_t* count);
+
+/* Sets the time bound of the encoders' cross-workgroup waits of this
+ * context (microseconds, 0 to 1e6; the default is KVSZP_WAIT_US or 200 us).
+ * A wait that outlasts it stops the launch, and the call is encoded again
+ * with the schedule that needs no residency (kvszp_reencode_count).  No
+ * reference counterpart: the reference's look-back spins without a bound
+ * (cuszp_batched_fixed.cu:256-275).  For callers that share the device with
+ * long-running kernels, and for tests that force the give-up path. */
+int kvszp_set_wait_bound(kvszp_ctx* ctx, double microseconds);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* kvszp_last_error(void);

@@ -66,6 +66,7 @@ constexpr int kSlots = 4;
 constexpr uint32_t kLinkDecodeGrid = 256;  // decoder workgroups reading pinned memory
 constexpr size_t kJobBalancedRuns = 1024;   // batches from this size: job-balanced decoder runs
 constexpr uint32_t kEpochLimit = (1u << 30) - 2u;
+constexpr double kMaxWaitMicros = 1e6;  // longest bound of a cross-workgroup wait
 constexpr uint64_t kMaxElements = 1ull << 29;      // per logical segment
 constexpr uint64_t kMaxTiles = (1ull << 32) / kThreads - 1;
 
@@ -95,7 +96,12 @@ struct kvszp_ctx {
     // ticks (KVSZP_WAIT_US, default 200 us), and how many calls were encoded
     // again after a launch gave up or overflowed.
     uint64_t wait_ticks = 0;
+    uint32_t clock_khz = 100000;  // device steady-clock rate
     uint64_t redone = 0;
+    // Epoch tags run from 1 to epoch_limit, then every tagged word is
+    // cleared and they start again (KVSZP_EPOCH_LIMIT lowers the limit so
+    // that tests can cross the wrap).
+    uint32_t epoch_limit = kEpochLimit;
     // Persistent encoder grid (co-resident workgroups); 0 = one workgroup
     // per tile (KVSZP_PERSISTENT=0, or ticket mode).
     uint32_t pipelined_grid = 0;
@@ -125,9 +131,16 @@ struct kvszp_ctx {
 
 namespace {
 
+// Device error words: encoder kernels (low half of control word 1) and
+// decoder kernels (high half), each with its own host marker.
 uint32_t* error_word(kvszp_ctx* c) {
     return reinterpret_cast<uint32_t*>(c->control + 1);
 }
+uint32_t* decode_error_word(kvszp_ctx* c) {
+    return reinterpret_cast<uint32_t*>(c->control + 1) + 1;
+}
+uint32_t* error_marker(kvszp_ctx* c) { return &c->host_ctl[kHostErrorMarker]; }
+uint32_t* decode_error_marker(kvszp_ctx* c) { return &c->host_ctl[kHostDecodeErrorMarker]; }
 
 // Epoch of the last launch of this context whose bounded waits gave up.
 unsigned long long* abort_word(kvszp_ctx* c) { return c->control + 2; }
@@ -143,11 +156,12 @@ int use_device(kvszp_ctx* c) {
     return KVSZP_OK;
 }
 
-// Grow-only device buffer.  New memory is zeroed when `zero` (epoch-tagged
-// words must never start with a tag that could match).
+// Grow-only device buffer, a whole number of 256-byte lines.  New memory is
+// zeroed when `zero` (epoch-tagged words must never start with a tag that
+// could match).
 int ensure(DevBuf& b, size_t bytes, bool zero, hipStream_t stream) {
     if (bytes <= b.bytes) return KVSZP_OK;
-    const size_t grown = std::max(bytes, b.bytes + b.bytes / 2);
+    const size_t grown = (std::max(bytes, b.bytes + b.bytes / 2) + 255) & ~(size_t)255;
     if (b.ptr) {
         hipError_t e = hipStreamSynchronize(stream);
         if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
@@ -163,8 +177,8 @@ int ensure(DevBuf& b, size_t bytes, bool zero, hipStream_t stream) {
     }
     b.bytes = grown;
     if (zero) {
-        e = hipMemsetAsync(b.ptr, 0, grown, stream);
-        if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync");
+        e = launch_fill_u64(static_cast<unsigned long long*>(b.ptr), grown / 8, stream);
+        if (e != hipSuccess) return hip_fail(e, "clearing a new workspace");
     }
     return KVSZP_OK;
 }
@@ -244,16 +258,25 @@ int upload_tables(kvszp_ctx* c, const void* data, size_t bytes, uint32_t seq,
     return KVSZP_OK;
 }
 
-// Next epoch tag; on wrap-around all tagged words are cleared first.
+// Next epoch tag.  When the tags run out, every word that holds one is
+// cleared before they start again: the look-back, min/max and flag words,
+// and the abort word, which holds the epoch of the last launch whose
+// bounded waits gave up (left standing, it would make every wait of the
+// next launch with that epoch give up without telling the host).  The
+// words are cleared by a fill kernel on `stream`, behind every earlier
+// launch of the context on it.
 int next_epoch(kvszp_ctx* c, hipStream_t stream, uint32_t* epoch) {
-    if (c->epoch >= kEpochLimit) {
+    if (c->epoch >= c->epoch_limit) {
         DevBuf* bufs[4] = {&c->tile_state, &c->tile_minmax, &c->job_minmax,
                            &c->job_flags};
         for (DevBuf* b : bufs) {
             if (!b->ptr) continue;
-            hipError_t e = hipMemsetAsync(b->ptr, 0, b->bytes, stream);
-            if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync");
+            hipError_t e = launch_fill_u64(static_cast<unsigned long long*>(b->ptr),
+                                           b->bytes / 8, stream);
+            if (e != hipSuccess) return hip_fail(e, "clearing the epoch words");
         }
+        hipError_t e = launch_fill_u64(abort_word(c), 1, stream);
+        if (e != hipSuccess) return hip_fail(e, "clearing the abort word");
         c->epoch = 0;
     }
     *epoch = ++c->epoch;
@@ -325,19 +348,25 @@ uint32_t header_bytes_of(uint64_t n) {
                       (kRefTileElems / kBlockElems));
 }
 
-// Reports (and clears) errors flagged by kernels of this context.  The
+// Reports (and clears) errors flagged by kernels of this context: those of
+// its encoder kernels, and with `decoders` also those of its decoders.  The
 // caller has synchronized `stream`, so no kernel of the context is running.
-// The device word is read only when a kernel raised the host marker.
-int consume_device_error(kvszp_ctx* c, hipStream_t stream) {
-    if (__atomic_load_n(&c->host_ctl[kHostErrorMarker], __ATOMIC_ACQUIRE) == 0)
-        return KVSZP_OK;
+// A device word is read only when a kernel raised its host marker.
+int consume_device_error(kvszp_ctx* c, hipStream_t stream, bool decoders = false) {
     uint32_t err = 0;
-    hipError_t e = hipMemcpyAsync(&err, error_word(c), sizeof(err),
-                                  hipMemcpyDeviceToHost, stream);
-    if (e == hipSuccess) e = hipMemsetAsync(error_word(c), 0, sizeof(uint32_t), stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(stream);
-    if (e != hipSuccess) return hip_fail(e, "reading the device error word");
-    __atomic_store_n(&c->host_ctl[kHostErrorMarker], 0u, __ATOMIC_RELEASE);
+    for (int side = 0; side < (decoders ? 2 : 1); ++side) {
+        uint32_t* marker = side ? decode_error_marker(c) : error_marker(c);
+        if (__atomic_load_n(marker, __ATOMIC_ACQUIRE) == 0) continue;
+        uint32_t* word = side ? decode_error_word(c) : error_word(c);
+        uint32_t bits = 0;
+        hipError_t e = hipMemcpyAsync(&bits, word, sizeof(bits), hipMemcpyDeviceToHost,
+                                      stream);
+        if (e == hipSuccess) e = hipMemsetAsync(word, 0, sizeof(uint32_t), stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) return hip_fail(e, "reading the device error word");
+        __atomic_store_n(marker, 0u, __ATOMIC_RELEASE);
+        err |= bits;
+    }
     if (!err) return KVSZP_OK;
     std::string what;
     if (err & kErrSpin) what += " bounded-wait-expired";
@@ -538,6 +567,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
             m.jobs = djobs;
             m.job_minmax = reinterpret_cast<unsigned long long*>(c->job_minmax.ptr);
             m.error = error_word(c);
+            m.error_marker = error_marker(c);
             m.host_ctl = c->host_ctl;
             m.seq = seq;
             m.epoch = epoch;
@@ -556,6 +586,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         p.host_redo = host_redo;
         p.job_flags = reinterpret_cast<uint32_t*>(c->job_flags.ptr);
         p.error = error_word(c);
+        p.error_marker = error_marker(c);
         p.host_ctl = c->host_ctl;
         p.seq = seq;
         p.ticket = c->use_tickets ? c->control : nullptr;
@@ -810,7 +841,8 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
             p.run_starts = reinterpret_cast<const uint32_t*>(
                 reinterpret_cast<char*>(c->tables.ptr) + runs_off);
         p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
-        p.error = error_word(c);
+        p.error = decode_error_word(c);
+        p.error_marker = decode_error_marker(c);
         p.host_ctl = c->host_ctl;
         p.seq = seq;
         p.ticket = c->use_tickets ? c->control : nullptr;
@@ -876,9 +908,15 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
         if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device_id) !=
                 hipSuccess || khz <= 0)
             khz = 100000;  // the steady counter of gfx9 parts runs at 100 MHz
+        c->clock_khz = (uint32_t)khz;
         const char* us = std::getenv("KVSZP_WAIT_US");
         const double wait_us = us ? std::atof(us) : 200.0;
-        c->wait_ticks = (uint64_t)(std::max(0.0, wait_us) * khz / 1000.0);
+        c->wait_ticks = (uint64_t)(std::min(kMaxWaitMicros, std::max(0.0, wait_us)) * khz /
+                                   1000.0);
+        if (const char* lim = std::getenv("KVSZP_EPOCH_LIMIT")) {
+            const long v = std::atol(lim);
+            if (v >= 2) c->epoch_limit = (uint32_t)std::min<long>(v, kEpochLimit);
+        }
     }
     e = hipMalloc(&c->control, 64);
     if (e == hipSuccess) e = hipMemset(c->control, 0, 64);
@@ -979,6 +1017,15 @@ int kvszp_set_options(kvszp_ctx* c, int quantizer, int rate0_policy) {
     return KVSZP_OK;
 }
 
+int kvszp_set_wait_bound(kvszp_ctx* c, double microseconds) {
+    if (!c) return fail(KVSZP_EINVAL, "null context");
+    if (!(microseconds >= 0.0 && microseconds <= kMaxWaitMicros))
+        return fail(KVSZP_EINVAL, "wait bound %g us outside [0, %g]", microseconds,
+                    kMaxWaitMicros);
+    c->wait_ticks = (uint64_t)(microseconds * c->clock_khz / 1000.0);
+    return KVSZP_OK;
+}
+
 size_t kvszp_estimate_compressed_buffer_size(size_t original_size) {
     return original_size * 2;
 }
@@ -1008,13 +1055,14 @@ static uint32_t g_scratch_epoch[64];
 static int scratch_epoch(kvszp_ctx* c, hipStream_t stream, uint32_t* epoch) {
     std::lock_guard<std::mutex> lock(g_scratch_epoch_mutex);
     uint32_t& cur = g_scratch_epoch[c->device];
-    if (cur >= kEpochLimit) {
+    if (cur >= c->epoch_limit) {
+        // Every tagged word: look-back, min/max, flags and the abort word.
         hipError_t e = launch_fill_u64(reinterpret_cast<unsigned long long*>(c->scratch),
                                        kScratchJobs / 8, stream);
         if (e == hipSuccess)
             e = launch_fill_u64(reinterpret_cast<unsigned long long*>(c->scratch +
                                                                      kScratchJobFlags),
-                                kNoAllocMaxJobs / 2, stream);
+                                (kScratchBytes - kScratchJobFlags) / 8, stream);
         if (e != hipSuccess) return hip_fail(e, "clearing the scratch words");
         cur = 0;
     }
@@ -1098,6 +1146,7 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
         m.jobs = djobs;
         m.job_minmax = words + kScratchJobMinMax / 8;
         m.error = error_word(c);
+        m.error_marker = error_marker(c);
         m.host_ctl = c->host_ctl;
         m.seq = seq;
         m.epoch = epoch;
@@ -1115,6 +1164,7 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
     p.host_redo = host_redo;
     p.job_flags = reinterpret_cast<uint32_t*>(c->scratch + kScratchJobFlags);
     p.error = error_word(c);
+    p.error_marker = error_marker(c);
     p.host_ctl = c->host_ctl;
     p.seq = seq;
     p.epoch = epoch;
@@ -1153,6 +1203,7 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
             m.jobs = djobs;
             m.job_minmax = words + kScratchJobMinMax / 8;
             m.error = error_word(c);
+            m.error_marker = error_marker(c);
             m.host_ctl = c->host_ctl;
             m.seq = seq;
             m.epoch = epoch;
@@ -1609,7 +1660,7 @@ int kvszp_synchronize(kvszp_ctx* c, kvszp_stream_t stream) {
     if (rc) return rc;
     hipError_t e = hipStreamSynchronize((hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    return consume_device_error(c, (hipStream_t)stream);
+    return consume_device_error(c, (hipStream_t)stream, true);
 }
 
 int kvszp_enable_timing(kvszp_ctx* c, int kinds) {

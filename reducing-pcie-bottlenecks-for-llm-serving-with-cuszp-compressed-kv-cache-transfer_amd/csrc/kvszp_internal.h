@@ -76,14 +76,18 @@ struct Group {
 
 // Host control block: pinned, coherent host memory that kernels write with
 // plain system-scope stores and the host reads after (or while) the stream
-// runs.  Word kHostErrorMarker becomes nonzero once any kernel flagged an
-// error (the bits themselves accumulate in the device error word);
-// word kHostSeq holds the sequence number of the last launch that started,
-// which tells the host that the table copy queued before it has completed.
+// runs.  Word kHostErrorMarker becomes nonzero once an encoder kernel
+// (min/max pre-pass, encoders) flagged an error, kHostDecodeErrorMarker once
+// a decoder did; the bits themselves accumulate in one device error word
+// per side, so that a compress call reports only what its own launches
+// found, not the errors of restores enqueued before it.  Word kHostSeq holds
+// the sequence number of the last launch that started, which tells the host
+// that the table copy queued before it has completed.
 constexpr int kHostErrorMarker = 0;
 constexpr int kHostSeq = 1;
 constexpr int kHostOverflow = 2;  // seq of a launch with jobs to encode again
 constexpr int kHostAbort = 3;     // seq of an encode whose bounded waits gave up
+constexpr int kHostDecodeErrorMarker = 4;
 constexpr int kHostCtlWords = 16;
 
 struct CompressJob {
@@ -110,6 +114,7 @@ struct CompressParams {
     uint32_t* host_redo;              // out (pinned host): seq = encode the job again
     uint32_t* job_flags;              // device, one per job: epoch = job marked
     uint32_t* error;                  // device error word (kErr* bits)
+    uint32_t* error_marker;           // its marker in the host control block
     uint32_t* host_ctl;               // pinned host control words, see above
     uint32_t seq;                     // launch sequence number
     unsigned long long* ticket;
@@ -136,6 +141,7 @@ struct MinMaxParams {
     const CompressJob* jobs;
     unsigned long long* job_minmax;   // two words per job: max key, ~min key
     uint32_t* error;
+    uint32_t* error_marker;
     uint32_t* host_ctl;
     uint32_t seq;
     uint32_t epoch;
@@ -150,6 +156,7 @@ struct DecompressParams {
     uint16_t* const* dests;           // kDstMulti destination table
     unsigned long long* tile_state;
     uint32_t* error;
+    uint32_t* error_marker;
     uint32_t* host_ctl;
     uint32_t seq;
     unsigned long long* ticket;

@@ -79,11 +79,10 @@ __device__ __forceinline__ void store_relaxed(unsigned long long* p,
 // Error reporting: the bits accumulate in the device word `e`; the host
 // control block gets a nonzero marker so the host learns of the error
 // without copying the device word back on every call.
-__device__ __forceinline__ void flag_error(uint32_t* e, uint32_t* host_ctl,
+__device__ __forceinline__ void flag_error(uint32_t* e, uint32_t* marker,
                                            uint32_t bits) {
     __hip_atomic_fetch_or(e, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&host_ctl[kHostErrorMarker], 1u, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(marker, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Time bound of a wait of the persistent encoder or of the fused bound
@@ -567,7 +566,7 @@ __device__ __forceinline__ const unsigned long long* lookback_first_addr(
 // set, nothing is published and the result is meaningless.
 __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
                                   uint32_t tile, uint32_t total, uint32_t epoch,
-                                  uint32_t* err, uint32_t* host_ctl,
+                                  uint32_t* err, uint32_t* err_marker,
                                   bool have_first = false, unsigned long long first = 0,
                                   const WaitBound* bound = nullptr,
                                   bool* gave_up = nullptr) {
@@ -605,7 +604,7 @@ __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
                     return 0;
                 }
             } else if (spins >= kSpinLimit) {
-                if (lane == 0) flag_error(err, host_ctl, kErrSpin);
+                if (lane == 0) flag_error(err, err_marker, kErrSpin);
                 need &= ready;
                 incl = 1;  // stop walking
                 break;
@@ -627,11 +626,11 @@ __device__ uint32_t lookback_wait(unsigned long long* state, uint32_t t,
 __device__ __forceinline__ uint32_t lookback(unsigned long long* state,
                                              uint32_t t, uint32_t tile,
                                              uint32_t total, uint32_t epoch,
-                                             uint32_t* err, uint32_t* host_ctl,
+                                             uint32_t* err, uint32_t* err_marker,
                                              const WaitBound* bound = nullptr,
                                              bool* gave_up = nullptr) {
     lookback_publish(state, t, tile, total, epoch);
-    return lookback_wait(state, t, tile, total, epoch, err, host_ctl, false, 0, bound,
+    return lookback_wait(state, t, tile, total, epoch, err, err_marker, false, 0, bound,
                          gave_up);
 }
 
@@ -822,7 +821,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     if (tid == 0) s_abort = 0;
     const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {  // tickets of another launch: never index past
-        if (tid == 0) flag_error(p.error, p.host_ctl, kErrSpin);
+        if (tid == 0) flag_error(p.error, p.error_marker, kErrSpin);
         return;
     }
     const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
@@ -894,7 +893,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
                             break;
                         }
                     } else if (spins >= kSpinLimit) {
-                        flag_error(p.error, p.host_ctl, kErrSpin);
+                        flag_error(p.error, p.error_marker, kErrSpin);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);
@@ -964,7 +963,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     if (wave == 0) {
         bool gave_up = false;
         const uint32_t prefix = lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error,
-                                         p.host_ctl, &bound, &gave_up);
+                                         p.error_marker, &bound, &gave_up);
         if (gave_up && lane == 0) s_abort = 1;
         if (lane == 0) {
             s_prefix = prefix;
@@ -976,8 +975,8 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
                                    __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
-    if (bad & 1) flag_error(p.error, p.host_ctl, kErrLayerIndex);
-    if (bad & 2) flag_error(p.error, p.host_ctl, kErrSpin);
+    if (bad & 1) flag_error(p.error, p.error_marker, kErrLayerIndex);
+    if (bad & 2) flag_error(p.error, p.error_marker, kErrSpin);
     __syncthreads();
     if (s_abort) return;
 
@@ -1103,7 +1102,7 @@ __global__ __launch_bounds__(kThreads) void compress_lorenzo_kernel(CompressPara
     if (tid == 0) s_abort = 0;
     const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {
-        if (tid == 0) flag_error(p.error, p.host_ctl, kErrSpin);
+        if (tid == 0) flag_error(p.error, p.error_marker, kErrSpin);
         return;
     }
     const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
@@ -1156,7 +1155,7 @@ __global__ __launch_bounds__(kThreads) void compress_lorenzo_kernel(CompressPara
     if (wave == 0) {
         bool gave_up = false;
         const uint32_t prefix = lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error,
-                                         p.host_ctl, &bound, &gave_up);
+                                         p.error_marker, &bound, &gave_up);
         if (gave_up && lane == 0) s_abort = 1;
         if (lane == 0) {
             s_prefix = prefix;
@@ -1168,7 +1167,7 @@ __global__ __launch_bounds__(kThreads) void compress_lorenzo_kernel(CompressPara
                                    __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
-    if (bad) flag_error(p.error, p.host_ctl, kErrSpin);
+    if (bad) flag_error(p.error, p.error_marker, kErrSpin);
     __syncthreads();
     if (s_abort) return;
 
@@ -1311,7 +1310,7 @@ __device__ __forceinline__ void load_block_regs(const CompressParams& p, const T
     const bool ex = live && block_exists(g, c.tile, wave * 64 + lane);
     uint32_t bad = 0;
     const uint64_t off = ex ? enc_block_source(g, c.tile, wave, lane, &bad) : 0;
-    if (bad) flag_error(p.error, p.host_ctl, kErrLayerIndex);
+    if (bad) flag_error(p.error, p.error_marker, kErrLayerIndex);
     const g_u32x4* src = ex ? (const g_u32x4*)to_global(job_of(p, c).in + off)
                             : (const g_u32x4*)to_global(&g_zero_block[0]);
 #pragma unroll
@@ -1570,7 +1569,7 @@ __device__ __forceinline__ bool job_keys(const CompressParams& p, uint32_t first
                     break;
                 }
             } else if (spins >= kSpinLimit) {
-                flag_error(p.error, p.host_ctl, kErrSpin);
+                flag_error(p.error, p.error_marker, kErrSpin);
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -1841,7 +1840,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
             const PendingTile& q = s_pend[parity ^ 1u];
             bool gave_up = false;
             const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                              p.epoch, p.error, p.host_ctl, true, probe,
+                                              p.epoch, p.error, p.error_marker, true, probe,
                                               &bound, &gave_up);
             if (gave_up && lane == 0) s_abort = 1;
             if (lane == 0) pending_results(p, q, pf, &s_prefix[parity]);
@@ -1939,7 +1938,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
                 const PendingTile& q = s_pend[parity ^ 1u];
                 bool gave_up = false;
                 const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                                  p.epoch, p.error, p.host_ctl, true, probe,
+                                                  p.epoch, p.error, p.error_marker, true, probe,
                                                   &bound, &gave_up);
                 if (gave_up && lane == 0) s_abort = 1;
                 if (lane == 0) pending_results(p, q, pf, &s_prefix[parity]);
@@ -2058,7 +2057,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
             const PendingTile& q = s_pend[parity];
             bool gave_up = false;
             const uint32_t pf = lookback_wait(p.tile_state, q.t, q.tile, q.total,
-                                              p.epoch, p.error, p.host_ctl, false, 0,
+                                              p.epoch, p.error, p.error_marker, false, 0,
                                               &bound, &gave_up);
             if (gave_up && lane == 0) s_abort = 1;
             if (lane == 0) pending_results(p, q, pf, &s_prefix[2]);
@@ -2140,7 +2139,7 @@ __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
                                tag | (key_max - kmin), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (bad) flag_error(p.error, p.host_ctl, kErrLayerIndex);
+    if (bad) flag_error(p.error, p.error_marker, kErrLayerIndex);
 }
 
 // ---- decoder ---------------------------------------------------------------
@@ -2535,7 +2534,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     publish_seq(p.host_ctl, p.seq);
     const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {
-        if (tid == 0) flag_error(p.error, p.host_ctl, kErrSpin);
+        if (tid == 0) flag_error(p.error, p.error_marker, kErrSpin);
         return;
     }
     const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
@@ -2568,7 +2567,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
     if (wave == 0) {
         const uint32_t pf = lookback(p.tile_state, t, tile, sc.total,
-                                     p.epoch, p.error, p.host_ctl);
+                                     p.epoch, p.error, p.error_marker);
         if (lane == 0) s_prefix = pf;
     }
     __syncthreads();
@@ -2594,7 +2593,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
                             wave_run_dst<kDst>(p, g, J, job, tile, wave), out,
                             &s_park[0][64 * wave], err);
     }
-    if (err) flag_error(p.error, p.host_ctl, err);
+    if (err) flag_error(p.error, p.error_marker, err);
 }
 
 // Decoder of the Lorenzo modes (specification above compress_lorenzo_kernel):
@@ -2613,7 +2612,7 @@ __global__ __launch_bounds__(kThreads) void decompress_lorenzo_kernel(Decompress
     publish_seq(p.host_ctl, p.seq);
     const uint32_t t = tile_number(p.ticket, p.ticket_base, &s_tile);
     if (t >= p.total_tiles) {
-        if (tid == 0) flag_error(p.error, p.host_ctl, kErrSpin);
+        if (tid == 0) flag_error(p.error, p.error_marker, kErrSpin);
         return;
     }
     const Group& g = p.groups[find_group(p.groups, p.num_groups, t)];
@@ -2646,7 +2645,7 @@ __global__ __launch_bounds__(kThreads) void decompress_lorenzo_kernel(Decompress
     const TileScan sc = tile_scan(bytes, tid, s_wave);  // has __syncthreads
     if (wave == 0) {
         const uint32_t pf = lookback(p.tile_state, t, tile, sc.total, p.epoch, p.error,
-                                     p.host_ctl);
+                                     p.error_marker);
         if (lane == 0) s_prefix = pf;
     }
     __syncthreads();
@@ -2694,7 +2693,7 @@ __global__ __launch_bounds__(kThreads) void decompress_lorenzo_kernel(Decompress
     }
     if (count != 0 && (hdr != 0 || p.rate0_zero))
         store_block_f32(reinterpret_cast<float*>(J.dst) + e0, out, count);
-    if (err) flag_error(p.error, p.host_ctl, err);
+    if (err) flag_error(p.error, p.error_marker, err);
 }
 
 // ---- persistent decoder ----------------------------------------------------
@@ -2852,7 +2851,7 @@ __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_
         cur = nxt;
         ++t;
     }
-    if (err) flag_error(p.error, p.host_ctl, err);
+    if (err) flag_error(p.error, p.error_marker, err);
 }
 
 // ---- packed publication ------------------------------------------------------

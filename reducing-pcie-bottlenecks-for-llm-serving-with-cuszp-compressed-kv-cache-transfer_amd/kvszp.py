@@ -87,6 +87,7 @@ EXPORTS = [
     ("kvszp_drain_timing", _i, [_vp, _vp, _vp, _vp, _vp]),
     ("kvszp_timing_durations", _i, [_vp, _i, _vp, _i, _vp]),
     ("kvszp_reencode_count", _i, [_vp, _vp]),
+    ("kvszp_set_wait_bound", _i, [_vp, ctypes.c_double]),
     ("kvszp_last_error", ctypes.c_char_p, []),
 ]
 
@@ -344,6 +345,10 @@ class Context:
         n = ctypes.c_uint64()
         check(self._lib.kvszp_reencode_count(self.handle, ctypes.byref(n)))
         return n.value
+
+    def set_wait_bound(self, microseconds: float) -> None:
+        """Time bound of the encoders' cross-workgroup waits (us)."""
+        check(self._lib.kvszp_set_wait_bound(self.handle, float(microseconds)))
 
     def synchronize(self, stream) -> int:
         return self._lib.kvszp_synchronize(self.handle, stream)

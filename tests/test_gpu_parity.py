@@ -469,6 +469,12 @@ def test_malformed_streams_are_reported(cpp):
     bad[3] = 40  # rate byte > 31
     assert w.decompress_batch_fixed_bf16([bad, bufs[1]], sizes, out, n, bounds)
     assert not w.synchronize()
+    # a store enqueued behind a bad restore reports only its own launches;
+    # the restore's error waits for synchronize()
+    assert w.decompress_batch_fixed_bf16([bad, bufs[1]], sizes, out, n, bounds)
+    ok, _, _ = w.compress_batch_fixed_bf16(list(pages), buffers(cpp, 2, n), [1e-4, 1e-4])
+    assert ok
+    assert not w.synchronize()
     short = [sizes[0] - 4, sizes[1]]
     assert w.decompress_batch_fixed_bf16(bufs, short, out, n, bounds)
     assert not w.synchronize()
