@@ -470,6 +470,62 @@ def pcie_steps(w: Grouped, steps: int) -> dict:
     return out
 
 
+def contended_store(w: Workload, calls: int = 16) -> dict:
+    """The store beside a busy stream: three BF16 products of 8192 x 8192
+    matrices queued on a second stream hold the CUs while the store runs on
+    the current stream, as the connector's store thread runs beside the
+    model's kernels (vllm_v1_compressed_offload.py:2365-2385).
+
+    Each call is classed by what the library did: "persistent" (the
+    persistent encoder ran through), "gave_up" (a bounded wait gave up and
+    the call was encoded again with the schedule that needs no residency),
+    "safe" (a recent give-up sent the call to that schedule at once).
+    Reported: the median wall time per class, solo (idle device) and
+    contended, and how many calls fell in each."""
+    torch = w.torch
+    a = torch.randn(8192, 8192, dtype=torch.bfloat16, device="cuda")
+    b = torch.randn(8192, 8192, dtype=torch.bfloat16, device="cuda")
+    busy = torch.cuda.Stream()
+
+    def one(contended: bool):
+        before = w.ctx.schedule_counts()
+        if contended:
+            with torch.cuda.stream(busy):
+                for _ in range(3):
+                    torch.mm(a, b)
+        t0 = time.perf_counter()
+        w.store(0)
+        ms = (time.perf_counter() - t0) * 1e3
+        torch.cuda.synchronize()
+        after = w.ctx.schedule_counts()
+        kind = ("gave_up" if after["reencoded"] > before["reencoded"]
+                else "safe" if after["safe_calls"] > before["safe_calls"] else "persistent")
+        return kind, ms
+
+    def summary(rows):
+        out = {}
+        for kind in ("persistent", "gave_up", "safe"):
+            ms = [m for k, m in rows if k == kind]
+            if ms:
+                out[kind] = {"calls": len(ms), "median_ms": round(statistics.median(ms), 4)}
+        return out
+
+    torch.cuda.synchronize()
+    solo = [one(False) for _ in range(calls)]
+    # one forced give-up (a zero wait bound), then the idle device's calls
+    # on the schedule that needs no residency
+    w.ctx.set_wait_bound(0.0)
+    forced = one(False)
+    w.ctx.set_wait_bound(200.0)
+    solo += [forced] + [one(False) for _ in range(calls)]
+    contended = [one(True) for _ in range(3 * calls)]
+    del a, b
+    torch.cuda.empty_cache()
+    return {"solo": summary(solo), "contended": summary(contended),
+            "busy_stream": "3 x torch.mm of 8192x8192 bf16 per call",
+            "wait_bound_us": 200.0}
+
+
 def uniform_ratio(w: Grouped) -> float:
     """Config 1's pages at a uniform REL 1e-4 (the metric's eb): one
     compress_batch_fixed_bf16 call over the 256 whole pages."""
@@ -692,6 +748,7 @@ def main() -> int:
                     help="config-1 pages of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-pcie", action="store_true")
+    ap.add_argument("--no-contended", action="store_true")
     ap.add_argument("--restore-per-group", action="store_true",
                     help="grouped configs: one indexed_scatter call per layer group "
                          "(the reference's call pattern) instead of one grouped launch")
@@ -740,15 +797,15 @@ def main() -> int:
     log(f"building config {args.config} ({sets} buffer sets)")
     w = make_workload(args.config, args.seed, sets, args.restore_per_group)
     log(f"{w.num_pages} pages x {w.page_numel} BF16, {w.batch} requests")
-    for i in range(max(1, warmup)):
-        w.step(i % sets)
-    torch.cuda.synchronize()
-    # The timed passes follow the warm-up directly.  Python's cyclic garbage
-    # collector stays off while they run (a full collection in a process
-    # holding torch takes milliseconds, and would land inside one step).
+    # The timed passes follow the warm-up directly (no idle gap before the
+    # first timed step).  Python's cyclic garbage collector stays off while
+    # they run (a full collection in a process holding torch takes
+    # milliseconds, and would land inside one step).
     gc.collect()
     gc.disable()
     try:
+        for i in range(max(1, warmup)):
+            w.step(i % sets)
         cold = timed_steps(w, steps, sets)
         warm = timed_steps(w, steps, 1) if sets > 1 else cold
     finally:
@@ -831,6 +888,9 @@ def main() -> int:
     }
     if args.config == 1:
         result["ratio_uniform_1e-4"] = uniform_ratio(w)
+        if not args.no_contended:
+            log("store beside a busy stream")
+            result["contended_store"] = contended_store(w)
         if not args.no_pcie:
             log("pcie store+restore")
             result["pcie"] = pcie_steps(w, 20)

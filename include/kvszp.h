@@ -341,6 +341,13 @@ int kvszp_timing_durations(kvszp_ctx* ctx, int kind, double* ms_out,
  * counterpart: the reference's kernels assume the launch runs alone. */
 int kvszp_reencode_count(const kvszp_ctx* ctx, uint64_t* count);
 
+/* Compress calls of this context encoded again after a give-up or a
+ * staging overflow (as kvszp_reencode_count), and compress calls that ran
+ * the schedule needing no residency from the start because a launch of the
+ * context gave up within the previous KVSZP_SAFE_CALLS calls (default 0:
+ * every call tries the persistent encoder).  No reference counterpart. */
+int kvszp_schedule_counts(const kvszp_ctx* ctx, uint64_t* reencoded, uint64_t* safe_calls);
+
 /* Sets the time bound of the encoders' cross-workgroup waits of this
  * context (microseconds, 0 to 1e6; the default is KVSZP_WAIT_US or 200 us).
  * A wait that outlasts it stops the launch, and the call is encoded again

@@ -98,6 +98,16 @@ struct kvszp_ctx {
     uint64_t wait_ticks = 0;
     uint32_t clock_khz = 100000;  // device steady-clock rate
     uint64_t redone = 0;
+    // After a launch gave up, the next `safe_after_abort` compress calls use
+    // the schedule that needs no residency straight away (KVSZP_SAFE_CALLS,
+    // default 0: off).  Measured on MI355X beside a stream of large matrix
+    // products, the persistent encoder did not give up and took 0.83 ms per
+    // configuration-1 store, the schedule that needs no residency 2.26 ms,
+    // so a give-up is not taken as a sign that the next call would give up
+    // too.  `safe_left` counts them down.
+    uint32_t safe_after_abort = 0;
+    uint32_t safe_left = 0;
+    uint64_t safe_calls = 0;      // compress calls run on that schedule
     // Epoch tags run from 1 to epoch_limit, then every tagged word is
     // cleared and they start again (KVSZP_EPOCH_LIMIT lowers the limit so
     // that tests can cross the wrap).
@@ -449,13 +459,15 @@ int fill_groups(Group* groups, const std::vector<GroupSpec>& specs, const Chunk&
 // API, cuszp_wrapper.cpp:216-429) instead of BF16 pages.
 // `safe`: only the schedule that needs no residency (pre-pass bound, one
 // workgroup per tile).  `mode` (fp32 only): kModeFixed, or the plain and
-// outlier residual codes of compress_lorenzo_kernel.
+// outlier residual codes of compress_lorenzo_kernel.  `bounds_given`: the
+// eps values are the jobs' absolute bounds, worked out already (used as
+// they are, also under a relative configuration).
 int compress_groups(kvszp_ctx* c, const void* const* inputs,
                     void* const* outputs, const uint64_t* capacities,
                     const float* eps_overrides, size_t batch,
                     const std::vector<GroupSpec>& specs, hipStream_t stream,
                     uint64_t* sizes_out, float* bounds_out, bool f32 = false,
-                    bool safe = false, int mode = kModeFixed) {
+                    bool safe = false, int mode = kModeFixed, bool bounds_given = false) {
     int rc = mode == kModeFixed ? check_fixed_config(c) : check_f32_config(c);
     if (rc) return rc;
     if (batch == 0) return fail(KVSZP_EINVAL, "empty batch");
@@ -499,7 +511,8 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
                             (unsigned long long)capacities[job],
                             (unsigned long long)need);
             if (in & 15u) aligned16 = false;
-            const float e = (eps_overrides && eps_overrides[job] > 0.0f)
+            const float e = bounds_given ? eps_overrides[job]
+                            : (eps_overrides && eps_overrides[job] > 0.0f)
                                 ? eps_overrides[job]
                                 : c->config.error_bound;  // cuszp_wrapper.cpp:473-479
             jobs[job].in = reinterpret_cast<const uint16_t*>(in);
@@ -517,7 +530,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         max_tiles = std::max(max_tiles, ch.tiles);
     }
 
-    const bool relative = c->config.use_relative_error != 0;
+    const bool relative = c->config.use_relative_error != 0 && !bounds_given;
     // Workspaces.
     if ((rc = ensure(c->tile_state, max_tiles * 8, true, stream)) ||
         (rc = ensure(c->tile_minmax, max_tiles * 8, true, stream)) ||
@@ -547,7 +560,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         for (size_t gi = chunks[k - 1].g0; gi < chunks[k - 1].g1; ++gi)
             chunk_first_job[k] += specs[gi].jobs;
     }
-    auto launch_chunk = [&](size_t k, bool safe) -> int {
+    auto launch_chunk = [&](size_t k, bool safe, bool timed) -> int {
         const Chunk& ch = chunks[k];
         CompressParams p;
         std::memset(&p, 0, sizeof(p));
@@ -559,7 +572,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         uint32_t epoch;
         int r = next_epoch(c, stream, &epoch);
         if (r) return r;
-        const int rec = safe ? -1 : timing_begin(c, KVSZP_KERNEL_COMPRESS);
+        const int rec = timed ? timing_begin(c, KVSZP_KERNEL_COMPRESS) : -1;
         hipError_t e;
         if (bound_mode == kBoundPrepass) {
             MinMaxParams m;
@@ -623,8 +636,16 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         c->ticket_next += ch.tiles;
         return KVSZP_OK;
     };
+    // A recent give-up on this context: the schedule that needs no residency
+    // for this call too (the device is likely still shared).
+    bool schedule_safe = safe;
+    if (!safe && !f32 && c->safe_left > 0) {
+        c->safe_left -= 1;
+        c->safe_calls += 1;
+        schedule_safe = true;
+    }
     for (size_t k = 0; k < chunks.size(); ++k)
-        if ((rc = launch_chunk(k, safe))) return rc;
+        if ((rc = launch_chunk(k, schedule_safe, true))) return rc;
 
     // The encoder wrote sizes and bounds into pinned host memory; wait for it,
     // since callers need the sizes on the host (cuszp_wrapper.cpp:520-532).
@@ -635,10 +656,11 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         // launches again with the schedule that needs no residency, under
         // fresh epochs.
         for (size_t k = 0; k < chunks.size(); ++k)
-            if (redo_candidate[k] && (rc = launch_chunk(k, true))) return rc;
+            if (redo_candidate[k] && (rc = launch_chunk(k, true, false))) return rc;
         e = wait_stream(stream);
         if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
         c->redone += 1;
+        c->safe_left = c->safe_after_abort;
     }
     rc = consume_device_error(c, stream);
     if (rc) return rc;
@@ -670,7 +692,9 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
                 in.push_back(inputs[j]);
                 out.push_back(outputs[j]);
                 cap.push_back(capacities ? capacities[j] : ~0ull);
-                eps.push_back(jobs[j].eps);
+                // the bound the launch worked out for the job (its first
+                // tile wrote it), so that the new launch needs no pre-pass
+                eps.push_back(bounds_out[j]);
                 where.push_back(j);
             }
         }
@@ -679,7 +703,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
             std::vector<float> eb(where.size());
             rc = compress_groups(c, in.data(), out.data(), cap.data(), eps.data(),
                                  where.size(), sub, stream, sz.data(), eb.data(), f32, true,
-                                 mode);
+                                 mode, true);
             if (rc) return rc;
             for (size_t k = 0; k < where.size(); ++k) {
                 sizes_out[where[k]] = sz[k];
@@ -913,6 +937,10 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
         const double wait_us = us ? std::atof(us) : 200.0;
         c->wait_ticks = (uint64_t)(std::min(kMaxWaitMicros, std::max(0.0, wait_us)) * khz /
                                    1000.0);
+        if (const char* sc = std::getenv("KVSZP_SAFE_CALLS")) {
+            const long v = std::atol(sc);
+            c->safe_after_abort = (uint32_t)std::max(0L, std::min(v, 1L << 20));
+        }
         if (const char* lim = std::getenv("KVSZP_EPOCH_LIMIT")) {
             const long v = std::atol(lim);
             if (v >= 2) c->epoch_limit = (uint32_t)std::min<long>(v, kEpochLimit);
@@ -1134,8 +1162,16 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
     g.tiles_per_job = tiles_per_job;
     g.header_bytes = header_bytes_of(n);
     p.num_groups = 1;
-    const int bound_mode = !relative ? kBoundAbsolute
-                           : (tiles_per_job <= c->fused_tile_limit ? kBoundFused : kBoundPrepass);
+    // After a recent give-up, the schedule that needs no residency at once.
+    const bool schedule_safe = c->safe_left > 0;
+    if (schedule_safe) {
+        c->safe_left -= 1;
+        c->safe_calls += 1;
+    }
+    const int bound_mode =
+        !relative ? kBoundAbsolute
+                  : (!schedule_safe && tiles_per_job <= c->fused_tile_limit ? kBoundFused
+                                                                            : kBoundPrepass);
     uint32_t* host_sizes = reinterpret_cast<uint32_t*>(c->noalloc_results);
     float* host_bounds = reinterpret_cast<float*>(host_sizes + kNoAllocMaxJobs);
     uint32_t* host_redo = host_sizes + 2 * kNoAllocMaxJobs;
@@ -1172,8 +1208,8 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
     p.bound_mode = bound_mode;
     p.quantizer = c->quantizer;
     p.aligned16 = aligned16 ? 1 : 0;
-    const bool persistent = bound_mode != kBoundPrepass && c->pipelined_grid != 0 &&
-                            whole_blocks && aligned16 &&
+    const bool persistent = !schedule_safe && bound_mode != kBoundPrepass &&
+                            c->pipelined_grid != 0 && whole_blocks && aligned16 &&
                             tiles_per_job <= c->pipelined_grid / 2;
     if (persistent || bound_mode == kBoundFused) {
         p.abort_word = words + kScratchAbort / 8;
@@ -1188,9 +1224,11 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
     if (e != hipSuccess) return hip_fail(e, "compress launch");
     e = wait_stream(stream);
     if (e != hipSuccess) return hip_fail(e, "waiting for the encoder");
+    const bool gave_up = p.abort_word != nullptr &&
+                         __atomic_load_n(&c->host_ctl[kHostAbort], __ATOMIC_ACQUIRE) == seq;
+    if (gave_up) c->safe_left = c->safe_after_abort;
     if (p.abort_word != nullptr &&
-        (__atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq ||
-         __atomic_load_n(&c->host_ctl[kHostAbort], __ATOMIC_ACQUIRE) == seq)) {
+        (gave_up || __atomic_load_n(&c->host_ctl[kHostOverflow], __ATOMIC_ACQUIRE) == seq)) {
         // Staging overflow, or a bounded wait gave up: the schedule that
         // needs no residency (pre-pass bound, one workgroup per tile).
         if ((rc = scratch_epoch(c, stream, &epoch))) return rc;
@@ -1726,6 +1764,13 @@ int kvszp_timing_durations(kvszp_ctx* c, int kind, double* ms_out, int capacity,
 int kvszp_reencode_count(const kvszp_ctx* c, uint64_t* count) {
     if (!c || !count) return fail(KVSZP_EINVAL, "null argument");
     *count = c->redone;
+    return KVSZP_OK;
+}
+
+int kvszp_schedule_counts(const kvszp_ctx* c, uint64_t* reencoded, uint64_t* safe_calls) {
+    if (!c || !reencoded || !safe_calls) return fail(KVSZP_EINVAL, "null argument");
+    *reencoded = c->redone;
+    *safe_calls = c->safe_calls;
     return KVSZP_OK;
 }
 

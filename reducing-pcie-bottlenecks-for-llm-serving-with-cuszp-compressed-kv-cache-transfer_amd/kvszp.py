@@ -88,6 +88,7 @@ EXPORTS = [
     ("kvszp_timing_durations", _i, [_vp, _i, _vp, _i, _vp]),
     ("kvszp_reencode_count", _i, [_vp, _vp]),
     ("kvszp_set_wait_bound", _i, [_vp, ctypes.c_double]),
+    ("kvszp_schedule_counts", _i, [_vp, _vp, _vp]),
     ("kvszp_last_error", ctypes.c_char_p, []),
 ]
 
@@ -345,6 +346,14 @@ class Context:
         n = ctypes.c_uint64()
         check(self._lib.kvszp_reencode_count(self.handle, ctypes.byref(n)))
         return n.value
+
+    def schedule_counts(self) -> dict:
+        """Compress calls encoded again (a give-up or a staging overflow)
+        and calls run on the schedule that needs no residency because of a
+        recent give-up."""
+        r, s = ctypes.c_uint64(), ctypes.c_uint64()
+        check(self._lib.kvszp_schedule_counts(self.handle, ctypes.byref(r), ctypes.byref(s)))
+        return {"reencoded": r.value, "safe_calls": s.value}
 
     def set_wait_bound(self, microseconds: float) -> None:
         """Time bound of the encoders' cross-workgroup waits (us)."""

@@ -1,8 +1,10 @@
 """The benchmark configurations other than the measured one, at full size,
 through the drop-in API (``cuszp_wrapper_cpp``).
 
-Config 1 (the bench workload) is checked by ``bench.py``'s round trip and by
-``test_pipeline_gpu.py``.  Here:
+Config 1 (the bench workload) is checked by ``bench.py``'s round trip and,
+every stream and restored value against the oracle, by
+``test_forward_progress_gpu.py::test_full_size_config1_store_and_restore_match_oracle``.
+Here:
 
 * config 0: one Qwen2.5-1.5B layer, K and V as two pages of 1 048 576
   values, REL 1e-4, contiguous restore -- small enough for the oracle to

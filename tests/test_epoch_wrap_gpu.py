@@ -12,7 +12,8 @@ the host, and that call would return without having written its streams.
 KVSZP_EPOCH_LIMIT lowers the limit to a few launches, so that the test
 crosses the wrap several times.  Launches before each wrap are made to give
 up from the host (a wait bound of zero; every kernel still exits normally),
-the launches after it run with the normal bound.  Output buffers are filled
+the launches after it run with the normal bound (KVSZP_SAFE_CALLS=0: no call
+skips the persistent encoder because an earlier one gave up).  Output buffers are filled
 with 0xAB before every call, so that a call which wrote nothing cannot pass
 on the previous call's bytes.  Every stream is checked against the oracle.
 """
@@ -47,6 +48,7 @@ def test_grouped_store_across_epoch_wraps(c1, monkeypatch):
     """The full configuration-1 store (512 segments, persistent encoder with
     the fused bound exchange) through two wraps of a 5-epoch context."""
     monkeypatch.setenv("KVSZP_EPOCH_LIMIT", str(LIMIT))
+    monkeypatch.setenv("KVSZP_SAFE_CALLS", "0")  # every call tries the persistent encoder
     w = fixed_wrapper()
     ctx = w._ctx
     req = c1_requests(c1)
@@ -73,6 +75,7 @@ def test_noalloc_across_epoch_wraps(oracle, monkeypatch):
     import kv_synth
 
     monkeypatch.setenv("KVSZP_EPOCH_LIMIT", str(LIMIT))
+    monkeypatch.setenv("KVSZP_SAFE_CALLS", "0")
     cfg = kvszp.Config(1e-4, 1, kvszp.DIM_1D, kvszp.MODE_FIXED, kvszp.TYPE_FLOAT)
     ctx = kvszp.Context(cfg, 0)
     pages = kv_synth.paged_kv(kv_synth.QWEN25_1P5B_4K, seed=5, device=DEV, tokens=16 * 64)

@@ -72,6 +72,7 @@ def test_forced_give_up_encodes_again_exactly(c1, monkeypatch):
     give up: the call is encoded again with the pre-pass schedule and must
     produce the same bytes."""
     monkeypatch.setenv("KVSZP_WAIT_US", "0")
+    monkeypatch.setenv("KVSZP_SAFE_CALLS", "0")
     w = _wrapper()
     req = _requests(c1)
     for _ in range(3):
@@ -97,6 +98,26 @@ def test_forced_give_up_encodes_again_exactly(c1, monkeypatch):
         want = oracle.compress_page(bits[i], n, float(eb))
         assert np.array_equal(bufs[i][:sizes[i]].cpu().numpy(), want), i
     assert w._ctx.reencode_count() >= before
+
+
+def test_calls_after_a_give_up_skip_the_persistent_encoder(c1, monkeypatch):
+    """After a launch gave up, the next KVSZP_SAFE_CALLS calls run the
+    schedule that needs no residency at once; then the persistent encoder is
+    tried again.  Every call's streams stay exact."""
+    monkeypatch.setenv("KVSZP_WAIT_US", "0")
+    monkeypatch.setenv("KVSZP_SAFE_CALLS", "2")
+    w = _wrapper()
+    req = _requests(c1)
+    seen = []
+    for _ in range(6):
+        req[1][0]._base.fill_(0xAB)
+        ok, sizes, bounds = _compress(w, c1, req)
+        assert ok
+        _check(c1, req[1], sizes, bounds)
+        seen.append(w._ctx.schedule_counts())
+    # give-up, safe, safe, give-up, safe, safe
+    assert [s["safe_calls"] for s in seen] == [0, 1, 2, 2, 3, 4]
+    assert seen[0]["reencoded"] >= 1 and seen[3]["reencoded"] == seen[0]["reencoded"] + 1
 
 
 def test_two_encoders_on_two_streams(c1):
