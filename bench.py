@@ -27,7 +27,7 @@ every pointer table built once and the pages resident in HBM:
 
 Reported (one JSON line):
   value            BF16 bytes of the job / wall time per step (store+restore)
-                   over K timed steps.  Each step uses the next of --rotate
+                   over K timed steps (per-step wall times in step_ms).  Each step uses the next of --rotate
                    buffer sets (pages, streams, destinations), so that a step
                    re-reads nothing the 256 MB Infinity Cache still holds from
                    the step before (default 3 sets for configs 0 and 1, whose
@@ -394,6 +394,8 @@ def timed_steps(w: Workload, steps: int, sets: int) -> dict:
         torch.cuda.synchronize()
         w.ctx.enable_timing(0)
         ms = w.ctx.timing_durations(kind)
+        if os.environ.get("KVSZP_BENCH_STEP_LOG"):
+            log(f"{key} us: " + " ".join(f"{x * 1e3:.1f}" for x in ms))
         per_step = len(ms) // steps if steps else 0
         out[key] = kernel_stats(ms)
         out[key]["launches_per_step"] = per_step
