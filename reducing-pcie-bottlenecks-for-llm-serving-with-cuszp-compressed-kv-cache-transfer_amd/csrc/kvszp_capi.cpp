@@ -539,8 +539,12 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         (rc = ensure_host_results(c, batch * 12)))
         return rc;
     const uint32_t seq = ++c->seq;
-    rc = upload_tables(c, jobs.data(), batch * sizeof(CompressJob), seq, stream);
-    if (rc) return rc;
+    // Small calls pass the job table in the kernel arguments (no upload).
+    const bool inline_jobs = batch <= (size_t)kInlineJobs;
+    if (!inline_jobs) {
+        rc = upload_tables(c, jobs.data(), batch * sizeof(CompressJob), seq, stream);
+        if (rc) return rc;
+    }
 
     uint32_t* host_sizes = reinterpret_cast<uint32_t*>(c->host_results);
     float* host_bounds = reinterpret_cast<float*>(host_sizes + batch);
@@ -578,6 +582,10 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
             MinMaxParams m;
             std::memset(&m, 0, sizeof(m));
             m.jobs = djobs;
+            if (inline_jobs) {
+                m.jobs_inline = 1;
+                std::memcpy(m.inline_jobs, jobs.data(), batch * sizeof(CompressJob));
+            }
             m.job_minmax = reinterpret_cast<unsigned long long*>(c->job_minmax.ptr);
             m.error = error_word(c);
             m.error_marker = error_marker(c);
@@ -591,6 +599,10 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
             if (e != hipSuccess) return hip_fail(e, "minmax launch");
         }
         p.jobs = djobs;
+        if (inline_jobs) {
+            p.jobs_inline = 1;
+            std::memcpy(p.inline_jobs, jobs.data(), batch * sizeof(CompressJob));
+        }
         p.tile_state = reinterpret_cast<unsigned long long*>(c->tile_state.ptr);
         p.tile_minmax = reinterpret_cast<unsigned long long*>(c->tile_minmax.ptr);
         p.job_minmax = reinterpret_cast<const unsigned long long*>(c->job_minmax.ptr);
@@ -825,7 +837,12 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         std::memcpy(table.data() + runs_off, runs.data(), runs.size() * sizeof(uint32_t));
     if ((rc = ensure(c->tile_state, max_tiles * 8, true, stream))) return rc;
     const uint32_t seq = ++c->seq;
-    if ((rc = upload_tables(c, table.data(), table.size(), seq, stream))) return rc;
+    // Small calls without a destination table or run starts pass their job
+    // table in the kernel arguments (no upload).
+    const bool inline_jobs =
+        batch <= (size_t)kInlineJobs && dest_table.empty() && runs.empty();
+    if (!inline_jobs && (rc = upload_tables(c, table.data(), table.size(), seq, stream)))
+        return rc;
 
     size_t first_job = 0;
     for (const Chunk& ch : chunks) {
@@ -859,6 +876,10 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         uint32_t epoch;
         if ((rc = next_epoch(c, stream, &epoch))) return rc;
         p.jobs = reinterpret_cast<const DecompressJob*>(c->tables.ptr);
+        if (inline_jobs) {
+            p.jobs_inline = 1;
+            std::memcpy(p.inline_jobs, jobs.data(), batch * sizeof(DecompressJob));
+        }
         p.dests = reinterpret_cast<uint16_t* const*>(
             reinterpret_cast<char*>(c->tables.ptr) + jobs_bytes);
         if (!runs.empty())
@@ -1144,9 +1165,14 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
     // The previous call on this context waited for its kernels, so the
     // staging records are free; the copy goes into the scratch job table.
     CompressJob* djobs = reinterpret_cast<CompressJob*>(c->scratch + kScratchJobs);
-    hipError_t e = hipMemcpyAsync(djobs, c->noalloc_stage, batch * sizeof(CompressJob),
-                                  hipMemcpyHostToDevice, stream);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D job table)");
+    // Small calls pass the job table in the kernel arguments instead.
+    const bool inline_jobs = batch <= (size_t)kInlineJobs;
+    hipError_t e = hipSuccess;
+    if (!inline_jobs) {
+        e = hipMemcpyAsync(djobs, c->noalloc_stage, batch * sizeof(CompressJob),
+                           hipMemcpyHostToDevice, stream);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D job table)");
+    }
     uint32_t epoch;
     if ((rc = scratch_epoch(c, stream, &epoch))) return rc;
 
@@ -1180,6 +1206,10 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
         MinMaxParams m;
         std::memset(&m, 0, sizeof(m));
         m.jobs = djobs;
+        if (inline_jobs) {
+            m.jobs_inline = 1;
+            std::memcpy(m.inline_jobs, c->noalloc_stage, batch * sizeof(CompressJob));
+        }
         m.job_minmax = words + kScratchJobMinMax / 8;
         m.error = error_word(c);
         m.error_marker = error_marker(c);
@@ -1192,6 +1222,10 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
         if (e != hipSuccess) return hip_fail(e, "minmax launch");
     }
     p.jobs = djobs;
+    if (inline_jobs) {
+        p.jobs_inline = 1;
+        std::memcpy(p.inline_jobs, c->noalloc_stage, batch * sizeof(CompressJob));
+    }
     p.tile_state = words + kScratchTileState / 8;
     p.tile_minmax = words + kScratchTileMinMax / 8;
     p.job_minmax = words + kScratchJobMinMax / 8;
@@ -1239,6 +1273,10 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
             MinMaxParams m;
             std::memset(&m, 0, sizeof(m));
             m.jobs = djobs;
+            if (inline_jobs) {
+                m.jobs_inline = 1;
+                std::memcpy(m.inline_jobs, c->noalloc_stage, batch * sizeof(CompressJob));
+            }
             m.job_minmax = words + kScratchJobMinMax / 8;
             m.error = error_word(c);
             m.error_marker = error_marker(c);

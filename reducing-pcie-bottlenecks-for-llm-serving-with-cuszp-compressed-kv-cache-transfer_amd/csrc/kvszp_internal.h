@@ -32,6 +32,9 @@ constexpr int kThreads = kTileBlocks;               // one thread per block
 constexpr int kTileElems = kTileBlocks * kBlockElems;
 constexpr int kRefTileElems = 32768;                // header granularity
 constexpr int kMaxGroups = 16;
+// Calls of at most this many jobs pass their job table in the kernel
+// arguments (no table upload before the launch).
+constexpr int kInlineJobs = 16;
 constexpr uint32_t kSpinLimit = 1u << 20;           // bounded waits (~1 s)
 
 // Device-side error bits (OR-ed into the context's error word).
@@ -135,6 +138,8 @@ struct CompressParams {
     unsigned long long* abort_word;
     uint64_t wait_ticks;
     Group groups[kMaxGroups];
+    int jobs_inline;                  // 1: the jobs are inline_jobs, not *jobs
+    CompressJob inline_jobs[kInlineJobs];
 };
 
 struct MinMaxParams {
@@ -149,6 +154,8 @@ struct MinMaxParams {
     int num_groups;
     int input_f32;                    // fp32 pages: 32-bit keys, NaN marked
     Group groups[kMaxGroups];         // first_tile is the first chunk
+    int jobs_inline;                  // 1: the jobs are inline_jobs, not *jobs
+    CompressJob inline_jobs[kInlineJobs];
 };
 
 struct DecompressParams {
@@ -182,6 +189,8 @@ struct DecompressParams {
     uint64_t weight_before[kMaxGroups];
     uint32_t tile_weight[kMaxGroups];
     Group groups[kMaxGroups];
+    int jobs_inline;                  // 1: the jobs are inline_jobs, not *jobs
+    DecompressJob inline_jobs[kInlineJobs];
 };
 
 // Packed publication: every payload i (src, size bytes) goes to

@@ -64,6 +64,14 @@ __device__ __forceinline__ T load_const(const T* table, uint32_t i) {
 #endif
 }
 
+// Job record i of a launch: from the kernel arguments for calls of at most
+// kInlineJobs jobs, else from the uploaded table (`jobs_inline` is uniform,
+// so this is a scalar branch).
+template <class Params>
+__device__ __forceinline__ auto job_at(const Params& p, uint32_t i) {
+    return p.jobs_inline ? p.inline_jobs[i] : load_const(p.jobs, i);
+}
+
 // ---- cross-workgroup primitives -------------------------------------------
 
 __device__ __forceinline__ unsigned long long load_relaxed(
@@ -830,7 +838,7 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressParams p) {
     const uint32_t job_in_group = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
     const uint32_t tile = local - job_in_group * g.tiles_per_job;
     const uint32_t job = g.first_job + job_in_group;
-    const CompressJob J = load_const(p.jobs, job);
+    const CompressJob J = job_at(p, job);
     const uint64_t n = g.n;
     const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
     const uint32_t b = tile * kTileBlocks + tid;
@@ -1110,7 +1118,7 @@ __global__ __launch_bounds__(kThreads) void compress_lorenzo_kernel(CompressPara
     const uint32_t job_in_group = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
     const uint32_t tile = local - job_in_group * g.tiles_per_job;
     const uint32_t job = g.first_job + job_in_group;
-    const CompressJob J = load_const(p.jobs, job);
+    const CompressJob J = job_at(p, job);
     const uint64_t n = g.n;
     const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
     const uint32_t b = tile * kTileBlocks + tid;
@@ -1240,7 +1248,7 @@ struct TileCtx {
 // the constant cache) rather than carried across the tile loop in scalar
 // registers.
 __device__ __forceinline__ CompressJob job_of(const CompressParams& p, const TileCtx& c) {
-    return load_const(p.jobs, c.job);
+    return job_at(p, c.job);
 }
 
 // Group lookup from first-tile numbers kept in LDS (a loop over kernel
@@ -2091,7 +2099,7 @@ __global__ __launch_bounds__(kThreads) void minmax_kernel(MinMaxParams p) {
     const uint32_t job_in_group = local / g.tiles_per_job;
     const uint32_t tile = local - job_in_group * g.tiles_per_job;
     const uint32_t job = g.first_job + job_in_group;
-    const CompressJob J = load_const(p.jobs, job);
+    const CompressJob J = job_at(p, job);
     const uint64_t n = g.n;
     const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
     const uint32_t b = tile * kTileBlocks + tid;
@@ -2542,7 +2550,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(
     const uint32_t job_in_group = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
     const uint32_t tile = local - job_in_group * g.tiles_per_job;
     const uint32_t job = g.first_job + job_in_group;
-    const DecompressJob J = load_const(p.jobs, job);
+    const DecompressJob J = job_at(p, job);
     const uint64_t n = g.n;
     const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
     const uint32_t b = tile * kTileBlocks + tid;
@@ -2620,7 +2628,7 @@ __global__ __launch_bounds__(kThreads) void decompress_lorenzo_kernel(Decompress
     const uint32_t job_in_group = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
     const uint32_t tile = local - job_in_group * g.tiles_per_job;
     const uint32_t job = g.first_job + job_in_group;
-    const DecompressJob J = load_const(p.jobs, job);
+    const DecompressJob J = job_at(p, job);
     const uint64_t n = g.n;
     const uint32_t nb = (uint32_t)((n + kBlockElems - 1) / kBlockElems);
     const uint32_t b = tile * kTileBlocks + tid;
@@ -2801,7 +2809,7 @@ __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_
     uint32_t hw;
     {
         const int tid = (int)threadIdx.x;
-        const uint8_t* in = load_const(p.jobs, cur.job).in;
+        const uint8_t* in = job_at(p, cur.job).in;
         if (cur.tile != 0) prefix = header_prefix(in, cur.tile, tid, s_red);
         hw = tile_header_word(in, cur.tile, tid);
     }
@@ -2809,7 +2817,7 @@ __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_
         const int tid = loop_tid();
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const Group& g = p.groups[cur.gi];
-        const DecompressJob J = load_const(p.jobs, cur.job);
+        const DecompressJob J = job_at(p, cur.job);
         // Segments hold fewer than 2^29 values: 32-bit element indices.
         const uint32_t n = (uint32_t)g.n;
         const uint32_t e0 = (cur.tile * kTileBlocks + (uint32_t)tid) * kBlockElems;
@@ -2836,7 +2844,7 @@ __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_
         DecTile nxt = cur;
         if (has_next) {
             nxt = dec_tile(p, t + 1, s_gfirst);
-            hw = tile_header_word(load_const(p.jobs, nxt.job).in, nxt.tile, tid);
+            hw = tile_header_word(job_at(p, nxt.job).in, nxt.tile, tid);
         }
         const uint32_t rmax = wave_max(rate);
         uint16_t* run = wave_run_dst<kDst>(p, g, J, cur.job, cur.tile, wave);
