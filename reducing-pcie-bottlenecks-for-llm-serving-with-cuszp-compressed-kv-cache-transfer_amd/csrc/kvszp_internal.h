@@ -150,7 +150,6 @@ struct MinMaxParams {
     uint32_t* host_ctl;
     uint32_t seq;
     uint32_t epoch;
-    uint32_t chunks_per_job;          // workgroups per job
     int num_groups;
     int input_f32;                    // fp32 pages: 32-bit keys, NaN marked
     Group groups[kMaxGroups];         // first_tile is the first chunk

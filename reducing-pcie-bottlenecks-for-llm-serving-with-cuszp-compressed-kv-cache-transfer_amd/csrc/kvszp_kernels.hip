@@ -2748,13 +2748,28 @@ __device__ __forceinline__ uint32_t tile_header_word(const uint8_t* in, uint32_t
 }
 
 // Payload bytes of the tiles [0, tile) of a job, from their rate bytes
-// (whole workgroup, one barrier; s_red holds one word per wave).
+// (whole workgroup, one barrier; s_red holds one word per wave).  A thread
+// reads its words 16 at a time with all 16 loads in flight (a loop of one
+// load per iteration waits out one memory round trip per word, e.g. 32 for
+// the last tile of a 128-tile job); indices past the header read word 0 and
+// count nothing, so every load is unconditional.
 __device__ __forceinline__ uint32_t header_prefix(const uint8_t* in, uint32_t tile,
                                                   int tid, uint32_t* s_red) {
+    constexpr int kBatch = 16;
     const g_u32* hw = to_global(reinterpret_cast<const uint32_t*>(in));
+    const uint32_t words = tile * (kTileBlocks / 4);
     uint32_t part = 0;
-    for (uint32_t i = (uint32_t)tid; i < tile * (kTileBlocks / 4); i += kThreads)
-        part += header_word_bytes(hw[i]);
+    for (uint32_t base = (uint32_t)tid; base < words; base += kBatch * kThreads) {
+        uint32_t v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const uint32_t i = base + (uint32_t)k * kThreads;
+            v[k] = hw[i < words ? i : 0u];
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k)
+            if (base + (uint32_t)k * kThreads < words) part += header_word_bytes(v[k]);
+    }
     part = wave_sum(part);
     if ((tid & 63) == 0) s_red[tid >> 6] = part;
     __syncthreads();
@@ -2963,6 +2978,32 @@ static void launch_block(void (*kernel)(Args...), uint32_t grid, uint32_t block,
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream, args...);
 }
 
+// The tile plan every tile loop indexes by: groups in launch order from
+// tile 0, each a whole number (at least one) of jobs numbered on from the
+// previous group's, together exactly `total_tiles`; and a grid of at least
+// one workgroup and, for the persistent kernels (a workgroup's first tile is
+// its own index), at most `total_tiles`.  Checked on the host before every
+// launch (at most kMaxGroups records), so that no kernel indexes job
+// records, layer maps or look-back words past a plan that does not add up.
+static bool tile_plan_ok(const Group* groups, int num_groups, uint32_t total_tiles,
+                         uint32_t grid, bool persistent) {
+    if (num_groups < 1 || num_groups > kMaxGroups || total_tiles == 0 || grid == 0) return false;
+    if (persistent && grid > total_tiles) return false;
+    if (groups[0].first_tile != 0) return false;
+    for (int i = 0; i < num_groups; ++i) {
+        const Group& g = groups[i];
+        const uint32_t end = i + 1 < num_groups ? groups[i + 1].first_tile : total_tiles;
+        if (end <= g.first_tile || g.tiles_per_job == 0 || g.n == 0) return false;
+        if ((g.n + kTileElems - 1) / kTileElems != g.tiles_per_job) return false;
+        const uint32_t tiles = end - g.first_tile;
+        if (tiles % g.tiles_per_job != 0) return false;
+        if (i + 1 < num_groups &&
+            groups[i + 1].first_job != g.first_job + tiles / g.tiles_per_job)
+            return false;
+    }
+    return true;
+}
+
 template <class... Args>
 static void launch(void (*kernel)(Args...), uint32_t grid, hipStream_t stream,
                    hipEvent_t start, hipEvent_t stop, Args... args) {
@@ -2971,6 +3012,8 @@ static void launch(void (*kernel)(Args...), uint32_t grid, hipStream_t stream,
 
 hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
                            hipEvent_t start, hipEvent_t stop) {
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, p.total_tiles, false))
+        return hipErrorInvalidValue;
     if (p.input_f32 && p.mode != kModeFixed) {
         if (p.mode == kModePlain) {
             if (p.quantizer)
@@ -2998,6 +3041,8 @@ hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
 hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
                                      hipStream_t stream, hipEvent_t start,
                                      hipEvent_t stop) {
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true))
+        return hipErrorInvalidValue;
     uint32_t longest = 0;
     for (int i = 0; i < p.num_groups; ++i) longest = std::max(longest, p.groups[i].tiles_per_job);
     if (longest <= kEarlyLookbackTiles) {
@@ -3020,6 +3065,8 @@ hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
 
 hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
                          hipStream_t stream, hipEvent_t start) {
+    if (!tile_plan_ok(p.groups, p.num_groups, grid, grid, false))  // one workgroup per tile
+        return hipErrorInvalidValue;
     if (p.input_f32)
         launch(minmax_kernel<1>, grid, stream, start, nullptr, p);
     else
@@ -3030,6 +3077,8 @@ hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
 hipError_t launch_decompress_persistent(const DecompressParams& p, uint32_t grid,
                                        hipStream_t stream, hipEvent_t start,
                                        hipEvent_t stop) {
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true))
+        return hipErrorInvalidValue;
     switch (p.dst_kind) {
     case kDstMulti:
         launch(decompress_persistent_kernel<kDstMulti>, grid, stream, start, stop, p);
@@ -3057,6 +3106,8 @@ int decompress_resident_workgroups(int device) {
 
 hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
                              hipEvent_t start, hipEvent_t stop) {
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, p.total_tiles, false))
+        return hipErrorInvalidValue;
     if (p.output_f32) {
         if (p.mode == kModePlain)
             launch(decompress_lorenzo_kernel<kModePlain>, p.total_tiles, stream, start, stop, p);
