@@ -76,13 +76,6 @@ struct TimingRecord {
     double bytes;  // algorithmic bytes of the launch (filled when known)
 };
 
-struct GroupSpec {
-    uint64_t n;
-    const int64_t* layers;
-    uint64_t sel, src, epl;
-    uint32_t jobs;
-};
-
 }  // namespace
 
 struct kvszp_ctx {
@@ -353,11 +346,6 @@ hipEvent_t timing_stop(kvszp_ctx* c, int rec) {
     return rec < 0 ? nullptr : c->timed[rec].stop;
 }
 
-uint32_t header_bytes_of(uint64_t n) {
-    return (uint32_t)((n + kRefTileElems - 1) / kRefTileElems *
-                      (kRefTileElems / kBlockElems));
-}
-
 // Reports (and clears) errors flagged by kernels of this context: those of
 // its encoder kernels, and with `decoders` also those of its decoders.  The
 // caller has synchronized `stream`, so no kernel of the context is running.
@@ -399,59 +387,6 @@ int validate_layers(const int64_t* layers, uint64_t sel, uint64_t prefix,
     if (sel * epl > 0xFFFFFFFFull - kTileElems)
         return fail(KVSZP_EINVAL, "selected layers x elements_per_layer too large");
     return KVSZP_OK;
-}
-
-// One launch's share of a call: groups [g0, g1) of the call's specs, with
-// job numbers global to the call and tile numbers local to the launch.
-struct Chunk {
-    size_t g0, g1;
-    uint64_t tiles;
-    uint32_t max_tiles_per_job;
-    bool whole_blocks;  // every block whole and inside one layer
-};
-
-// Splits `specs` into launches of at most kMaxGroups groups (the group
-// records travel as kernel arguments).  The reference takes any number of
-// groups (cuszp_wrapper.cpp:683-868, one launch per group).
-std::vector<Chunk> split_chunks(const std::vector<GroupSpec>& specs) {
-    std::vector<Chunk> chunks;
-    for (size_t g0 = 0; g0 < specs.size(); g0 += kMaxGroups) {
-        Chunk ch{g0, std::min(specs.size(), g0 + (size_t)kMaxGroups), 0, 0, true};
-        for (size_t gi = ch.g0; gi < ch.g1; ++gi) {
-            const GroupSpec& s = specs[gi];
-            const uint32_t tpj = (uint32_t)((s.n + kTileElems - 1) / kTileElems);
-            ch.tiles += (uint64_t)tpj * s.jobs;
-            ch.max_tiles_per_job = std::max(ch.max_tiles_per_job, tpj);
-            if ((s.n % kBlockElems) != 0 || (s.layers && (s.epl % kBlockElems) != 0))
-                ch.whole_blocks = false;
-        }
-        chunks.push_back(ch);
-    }
-    return chunks;
-}
-
-// Group records of one chunk; `first_job` is the call-wide job number of
-// the chunk's first request.
-int fill_groups(Group* groups, const std::vector<GroupSpec>& specs, const Chunk& ch,
-                size_t first_job) {
-    uint64_t tiles = 0;
-    size_t job = first_job;
-    for (size_t gi = ch.g0; gi < ch.g1; ++gi) {
-        const GroupSpec& s = specs[gi];
-        Group& g = groups[gi - ch.g0];
-        g.n = s.n;
-        g.layers = s.layers;
-        g.selected_layers = s.sel;
-        g.source_layers = s.src;
-        g.elements_per_layer = s.epl;
-        g.first_job = (uint32_t)job;
-        g.first_tile = (uint32_t)tiles;
-        g.tiles_per_job = (uint32_t)((s.n + kTileElems - 1) / kTileElems);
-        g.header_bytes = header_bytes_of(s.n);
-        tiles += (uint64_t)g.tiles_per_job * s.jobs;
-        job += s.jobs;
-    }
-    return (int)(ch.g1 - ch.g0);
 }
 
 // Common compress path: `specs` are the groups, requests laid out group by
@@ -582,6 +517,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
             MinMaxParams m;
             std::memset(&m, 0, sizeof(m));
             m.jobs = djobs;
+            m.num_jobs = (uint32_t)batch;
             if (inline_jobs) {
                 m.jobs_inline = 1;
                 std::memcpy(m.inline_jobs, jobs.data(), batch * sizeof(CompressJob));
@@ -599,6 +535,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
             if (e != hipSuccess) return hip_fail(e, "minmax launch");
         }
         p.jobs = djobs;
+        p.num_jobs = (uint32_t)batch;
         if (inline_jobs) {
             p.jobs_inline = 1;
             std::memcpy(p.inline_jobs, jobs.data(), batch * sizeof(CompressJob));
@@ -788,39 +725,7 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     if (persistent && chunks.size() == 1 && batch >= kJobBalancedRuns && chunks[0].tiles > 0) {
         uint32_t grid = (uint32_t)std::min<uint64_t>(chunks[0].tiles, c->decompress_grid);
         if (grid_cap) grid = std::min(grid, grid_cap);
-        std::vector<uint64_t> bytes(batch);
-        std::vector<uint32_t> tiles_of(batch);
-        uint64_t total = 0;
-        size_t j = 0;
-        for (const GroupSpec& spec : specs) {
-            const uint32_t R = header_bytes_of(spec.n);
-            const uint32_t tpj = (uint32_t)((spec.n + kTileElems - 1) / kTileElems);
-            for (uint32_t k = 0; k < spec.jobs; ++k, ++j) {
-                bytes[j] = 2 * spec.n + (sizes[j] - R);
-                tiles_of[j] = tpj;
-                total += bytes[j];
-            }
-        }
-        runs.resize((size_t)grid + 1);
-        size_t jj = 0;
-        uint64_t before = 0;
-        uint64_t tile_before = 0;
-        for (uint32_t b = 0; b < grid; ++b) {
-            const uint64_t target = (uint64_t)((unsigned __int128)b * total / grid);
-            while (jj < batch && before + bytes[jj] <= target) {
-                before += bytes[jj];
-                tile_before += tiles_of[jj];
-                ++jj;
-            }
-            if (jj == batch) {
-                runs[b] = (uint32_t)chunks[0].tiles;
-            } else {
-                const uint64_t i = (uint64_t)(((unsigned __int128)(target - before) * tiles_of[jj] +
-                                               bytes[jj] - 1) / bytes[jj]);
-                runs[b] = (uint32_t)(tile_before + std::min<uint64_t>(i, tiles_of[jj]));
-            }
-        }
-        runs[grid] = (uint32_t)chunks[0].tiles;
+        runs = job_balanced_runs(specs, sizes, batch, chunks[0].tiles, grid);
     }
 
     // Packed table: jobs, then (kDstMulti) the destination pointers, then
@@ -853,29 +758,14 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         // group's average payload per tile), so that workgroups holding tiles
         // of a high-rate group get fewer of them.  Kernel arguments only: the
         // table keeps its size.
-        {
-            uint64_t before = 0;
-            size_t j = first_job;
-            for (size_t gi = ch.g0; gi < ch.g1; ++gi) {
-                const GroupSpec& spec = specs[gi];
-                const Group& g = p.groups[gi - ch.g0];
-                uint64_t payload = 0;
-                for (uint32_t k = 0; k < spec.jobs; ++k, ++j) payload += sizes[j] - g.header_bytes;
-                const uint64_t tiles = (uint64_t)g.tiles_per_job * spec.jobs;
-                // Callers reject empty groups; the guard keeps the division defined.
-                const uint64_t w =
-                    tiles ? (2 * spec.n * spec.jobs + payload + tiles / 2) / tiles : 1;
-                p.tile_weight[gi - ch.g0] = (uint32_t)std::max<uint64_t>(w, 1);
-                p.weight_before[gi - ch.g0] = before;
-                before += tiles * p.tile_weight[gi - ch.g0];
-            }
-            p.total_weight = before;
-        }
+        p.total_weight = group_tile_weights(p.groups, p.num_groups, specs, ch, sizes,
+                                            p.weight_before, p.tile_weight);
         for (size_t gi = ch.g0; gi < ch.g1; ++gi) first_job += specs[gi].jobs;
         if (ch.tiles == 0) continue;
         uint32_t epoch;
         if ((rc = next_epoch(c, stream, &epoch))) return rc;
         p.jobs = reinterpret_cast<const DecompressJob*>(c->tables.ptr);
+        p.num_jobs = (uint32_t)batch;
         if (inline_jobs) {
             p.jobs_inline = 1;
             std::memcpy(p.inline_jobs, jobs.data(), batch * sizeof(DecompressJob));
@@ -1206,6 +1096,7 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
         MinMaxParams m;
         std::memset(&m, 0, sizeof(m));
         m.jobs = djobs;
+        m.num_jobs = (uint32_t)batch;
         if (inline_jobs) {
             m.jobs_inline = 1;
             std::memcpy(m.inline_jobs, c->noalloc_stage, batch * sizeof(CompressJob));
@@ -1222,6 +1113,7 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
         if (e != hipSuccess) return hip_fail(e, "minmax launch");
     }
     p.jobs = djobs;
+    p.num_jobs = (uint32_t)batch;
     if (inline_jobs) {
         p.jobs_inline = 1;
         std::memcpy(p.inline_jobs, c->noalloc_stage, batch * sizeof(CompressJob));
@@ -1273,6 +1165,7 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
             MinMaxParams m;
             std::memset(&m, 0, sizeof(m));
             m.jobs = djobs;
+            m.num_jobs = (uint32_t)batch;
             if (inline_jobs) {
                 m.jobs_inline = 1;
                 std::memcpy(m.inline_jobs, c->noalloc_stage, batch * sizeof(CompressJob));

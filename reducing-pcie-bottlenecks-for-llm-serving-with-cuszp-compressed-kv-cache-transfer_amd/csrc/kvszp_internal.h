@@ -1,14 +1,6 @@
 // kvszp_internal.h -- launch descriptors shared by the HIP kernels
-// (kvszp_kernels.hip) and the host C-ABI (kvszp_capi.cpp).
-//
-// Work decomposition.  A "job" is one logical segment to encode or decode
-// (one page, or the layer-selected part of one page).  Jobs with the same
-// geometry form a "group".  Every job is cut into tiles of kTileBlocks
-// fixed-rate blocks (kTileBlocks * 32 elements); one workgroup of
-// kTileBlocks threads handles one tile, one thread per 32-element block.
-// Tiles are numbered group by group, job by job, so the tiles of a job are
-// consecutive.  A launch holds at most kMaxGroups groups (the records are
-// kernel arguments); the host splits larger calls into several launches.
+// (kvszp_kernels.hip) and the host C-ABI (kvszp_capi.cpp).  Groups, jobs,
+// tiles and their numbering: kvszp_plan.h.
 //
 // Schedules.  By default the one-workgroup-per-tile kernels take tile =
 // blockIdx.x; their only cross-workgroup waits are on tiles of lower
@@ -24,14 +16,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kvszp_plan.h"
+
 namespace kvszp {
 
-constexpr int kBlockElems = 32;                     // fixed-rate block
-constexpr int kTileBlocks = 256;                    // blocks per tile
 constexpr int kThreads = kTileBlocks;               // one thread per block
-constexpr int kTileElems = kTileBlocks * kBlockElems;
-constexpr int kRefTileElems = 32768;                // header granularity
-constexpr int kMaxGroups = 16;
 // Calls of at most this many jobs pass their job table in the kernel
 // arguments (no table upload before the launch).
 constexpr int kInlineJobs = 16;
@@ -63,18 +52,6 @@ enum : int {
     kDstLinear = 0,        // element e -> dst + e
     kDstMulti = 1,         // element e -> dests[job*dpp + e/epd] + e%epd
     kDstIndexed = 2,       // element e -> dst + layer-mapped index
-};
-
-struct Group {
-    uint64_t n;                 // logical elements per job
-    const int64_t* layers;      // device layer map, nullptr = contiguous
-    uint64_t selected_layers;
-    uint64_t source_layers;
-    uint64_t elements_per_layer;
-    uint32_t first_job;
-    uint32_t first_tile;
-    uint32_t tiles_per_job;
-    uint32_t header_bytes;      // R = 1024 * ceil(n / 32768)
 };
 
 // Host control block: pinned, coherent host memory that kernels write with
@@ -138,6 +115,7 @@ struct CompressParams {
     unsigned long long* abort_word;
     uint64_t wait_ticks;
     Group groups[kMaxGroups];
+    uint32_t num_jobs;                // job records in the table (jobs or inline_jobs)
     int jobs_inline;                  // 1: the jobs are inline_jobs, not *jobs
     CompressJob inline_jobs[kInlineJobs];
 };
@@ -153,6 +131,7 @@ struct MinMaxParams {
     int num_groups;
     int input_f32;                    // fp32 pages: 32-bit keys, NaN marked
     Group groups[kMaxGroups];         // first_tile is the first chunk
+    uint32_t num_jobs;                // job records in the table (jobs or inline_jobs)
     int jobs_inline;                  // 1: the jobs are inline_jobs, not *jobs
     CompressJob inline_jobs[kInlineJobs];
 };
@@ -188,6 +167,7 @@ struct DecompressParams {
     uint64_t weight_before[kMaxGroups];
     uint32_t tile_weight[kMaxGroups];
     Group groups[kMaxGroups];
+    uint32_t num_jobs;                // job records in the table (jobs or inline_jobs)
     int jobs_inline;                  // 1: the jobs are inline_jobs, not *jobs
     DecompressJob inline_jobs[kInlineJobs];
 };

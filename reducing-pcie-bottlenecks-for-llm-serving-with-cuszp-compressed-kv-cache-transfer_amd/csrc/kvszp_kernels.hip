@@ -1255,17 +1255,12 @@ __device__ __forceinline__ CompressJob job_of(const CompressParams& p, const Til
 // arguments would keep all of them in scalar registers across the tile loop).
 __device__ __forceinline__ TileCtx tile_ctx(const CompressParams& p, uint32_t t,
                                             const uint32_t* s_gfirst) {
+    const TilePlace pl = place_tile(p.groups, s_gfirst, p.num_groups, t);
     TileCtx c;
     c.t = t;
-    int gi = 0;
-    for (int i = 1; i < p.num_groups; ++i)
-        if (t >= s_gfirst[i]) gi = i;
-    c.gi = __builtin_amdgcn_readfirstlane(gi);
-    const Group& g = p.groups[c.gi];
-    const uint32_t local = t - g.first_tile;
-    const uint32_t jig = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
-    c.tile = local - jig * g.tiles_per_job;
-    c.job = g.first_job + jig;
+    c.gi = pl.gi;
+    c.job = pl.job;
+    c.tile = pl.tile;
     return c;
 }
 
@@ -2726,16 +2721,11 @@ struct DecTile {
 
 __device__ __forceinline__ DecTile dec_tile(const DecompressParams& p, uint32_t t,
                                             const uint32_t* s_gfirst) {
+    const TilePlace pl = place_tile(p.groups, s_gfirst, p.num_groups, t);
     DecTile c;
-    int gi = 0;
-    for (int i = 1; i < p.num_groups; ++i)
-        if (t >= s_gfirst[i]) gi = i;
-    c.gi = __builtin_amdgcn_readfirstlane(gi);
-    const Group& g = p.groups[c.gi];
-    const uint32_t local = t - g.first_tile;
-    const uint32_t jig = __builtin_amdgcn_readfirstlane(local / g.tiles_per_job);
-    c.tile = local - jig * g.tiles_per_job;
-    c.job = g.first_job + jig;
+    c.gi = pl.gi;
+    c.job = pl.job;
+    c.tile = pl.tile;
     return c;
 }
 
@@ -2779,25 +2769,13 @@ __device__ __forceinline__ uint32_t header_prefix(const uint8_t* in, uint32_t ti
     return total;
 }
 
-// First tile of workgroup b's run out of G: the tile where the cumulative
-// weight reaches b/G of the total (rounded up), so that every workgroup
-// moves about the same number of bytes.  Nondecreasing in b, 0 at b = 0
-// and total_tiles at b = G, so the runs tile [0, total_tiles) exactly.
+// First tile of workgroup b's run out of G: the host's per-workgroup run
+// table, or the run balanced by the per-group tile weights.
 __device__ __forceinline__ uint32_t run_start(const DecompressParams& p, uint32_t b,
                                               uint32_t G) {
     if (p.run_starts != nullptr) return load_const(p.run_starts, b < G ? b : G);
-    if (p.total_weight == 0) return (uint32_t)((uint64_t)b * p.total_tiles / G);
-    if (b >= G) return p.total_tiles;
-    const uint64_t target = (uint64_t)b * p.total_weight / G;
-    int g = 0;
-    for (int k = 1; k < p.num_groups; ++k)
-        if (p.weight_before[k] <= target) g = k;
-    const uint32_t first = p.groups[g].first_tile;
-    const uint32_t tiles =
-        (g + 1 < p.num_groups ? p.groups[g + 1].first_tile : p.total_tiles) - first;
-    const uint64_t w = p.tile_weight[g];
-    const uint64_t i = (target - p.weight_before[g] + w - 1) / w;
-    return first + (uint32_t)(i < tiles ? i : tiles);
+    return weighted_run_start(p.groups, p.num_groups, p.total_tiles, p.total_weight,
+                              p.weight_before, p.tile_weight, b, G);
 }
 
 template <int kDst>
@@ -2978,30 +2956,12 @@ static void launch_block(void (*kernel)(Args...), uint32_t grid, uint32_t block,
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream, args...);
 }
 
-// The tile plan every tile loop indexes by: groups in launch order from
-// tile 0, each a whole number (at least one) of jobs numbered on from the
-// previous group's, together exactly `total_tiles`; and a grid of at least
-// one workgroup and, for the persistent kernels (a workgroup's first tile is
-// its own index), at most `total_tiles`.  Checked on the host before every
-// launch (at most kMaxGroups records), so that no kernel indexes job
-// records, layer maps or look-back words past a plan that does not add up.
-static bool tile_plan_ok(const Group* groups, int num_groups, uint32_t total_tiles,
-                         uint32_t grid, bool persistent) {
-    if (num_groups < 1 || num_groups > kMaxGroups || total_tiles == 0 || grid == 0) return false;
-    if (persistent && grid > total_tiles) return false;
-    if (groups[0].first_tile != 0) return false;
-    for (int i = 0; i < num_groups; ++i) {
-        const Group& g = groups[i];
-        const uint32_t end = i + 1 < num_groups ? groups[i + 1].first_tile : total_tiles;
-        if (end <= g.first_tile || g.tiles_per_job == 0 || g.n == 0) return false;
-        if ((g.n + kTileElems - 1) / kTileElems != g.tiles_per_job) return false;
-        const uint32_t tiles = end - g.first_tile;
-        if (tiles % g.tiles_per_job != 0) return false;
-        if (i + 1 < num_groups &&
-            groups[i + 1].first_job != g.first_job + tiles / g.tiles_per_job)
-            return false;
-    }
-    return true;
+// Job records a kernel of these parameters can read (0 when an inline table
+// is said to hold more than it can).
+template <class Params>
+static uint32_t readable_jobs(const Params& p) {
+    return p.jobs_inline ? (p.num_jobs <= (uint32_t)kInlineJobs ? p.num_jobs : 0u)
+                         : (p.jobs != nullptr ? p.num_jobs : 0u);
 }
 
 template <class... Args>
@@ -3012,7 +2972,8 @@ static void launch(void (*kernel)(Args...), uint32_t grid, hipStream_t stream,
 
 hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
                            hipEvent_t start, hipEvent_t stop) {
-    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, p.total_tiles, false))
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, p.total_tiles, false,
+                      readable_jobs(p)))
         return hipErrorInvalidValue;
     if (p.input_f32 && p.mode != kModeFixed) {
         if (p.mode == kModePlain) {
@@ -3041,7 +3002,7 @@ hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
 hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
                                      hipStream_t stream, hipEvent_t start,
                                      hipEvent_t stop) {
-    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true))
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true, readable_jobs(p)))
         return hipErrorInvalidValue;
     uint32_t longest = 0;
     for (int i = 0; i < p.num_groups; ++i) longest = std::max(longest, p.groups[i].tiles_per_job);
@@ -3065,7 +3026,7 @@ hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
 
 hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
                          hipStream_t stream, hipEvent_t start) {
-    if (!tile_plan_ok(p.groups, p.num_groups, grid, grid, false))  // one workgroup per tile
+    if (!tile_plan_ok(p.groups, p.num_groups, grid, grid, false, readable_jobs(p)))  // a workgroup per tile
         return hipErrorInvalidValue;
     if (p.input_f32)
         launch(minmax_kernel<1>, grid, stream, start, nullptr, p);
@@ -3077,7 +3038,7 @@ hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
 hipError_t launch_decompress_persistent(const DecompressParams& p, uint32_t grid,
                                        hipStream_t stream, hipEvent_t start,
                                        hipEvent_t stop) {
-    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true))
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true, readable_jobs(p)))
         return hipErrorInvalidValue;
     switch (p.dst_kind) {
     case kDstMulti:
@@ -3106,7 +3067,8 @@ int decompress_resident_workgroups(int device) {
 
 hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
                              hipEvent_t start, hipEvent_t stop) {
-    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, p.total_tiles, false))
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, p.total_tiles, false,
+                      readable_jobs(p)))
         return hipErrorInvalidValue;
     if (p.output_f32) {
         if (p.mode == kModePlain)

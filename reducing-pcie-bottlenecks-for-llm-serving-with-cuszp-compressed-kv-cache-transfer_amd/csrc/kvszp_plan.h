@@ -1,0 +1,285 @@
+// kvszp_plan.h -- the tile plan of a launch: how a call's requests become
+// groups, jobs and tiles, which group, job and tile of the job a tile number
+// stands for, and where each workgroup of the persistent decoder starts.
+// Shared by the kernels (the device lookups), the host C-ABI (which builds
+// the plan) and a host test that walks every tile of random plans with
+// bounds checks.  No HIP headers: the host parts build with g++ alone.
+//
+// A "job" is one logical segment to encode or decode (one page, or the
+// layer-selected part of one page).  Jobs with the same geometry form a
+// "group".  Every job is cut into tiles of kTileBlocks fixed-rate blocks;
+// tiles are numbered group by group, job by job, so the tiles of a job are
+// consecutive.  A launch holds at most kMaxGroups groups (the records are
+// kernel arguments); the host splits larger calls into several launches.
+#ifndef KVSZP_PLAN_H
+#define KVSZP_PLAN_H
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define KVSZP_PLAN_FN __host__ __device__ __forceinline__
+#else
+#define KVSZP_PLAN_FN static inline
+#endif
+
+// A value every lane of a wave holds alike, moved to a scalar register on
+// the device (so that what it indexes is read with scalar loads).
+#if defined(__HIP_DEVICE_COMPILE__)
+#define KVSZP_UNIFORM(x) __builtin_amdgcn_readfirstlane(x)
+#else
+#define KVSZP_UNIFORM(x) (x)
+#endif
+
+#include <algorithm>
+#include <vector>
+
+namespace kvszp {
+
+constexpr int kBlockElems = 32;                     // fixed-rate block
+constexpr int kTileBlocks = 256;                    // blocks per tile
+constexpr int kTileElems = kTileBlocks * kBlockElems;
+constexpr int kRefTileElems = 32768;                // header granularity
+constexpr int kMaxGroups = 16;
+
+struct Group {
+    uint64_t n;                 // logical elements per job
+    const int64_t* layers;      // device layer map, nullptr = contiguous
+    uint64_t selected_layers;
+    uint64_t source_layers;
+    uint64_t elements_per_layer;
+    uint32_t first_job;
+    uint32_t first_tile;
+    uint32_t tiles_per_job;
+    uint32_t header_bytes;      // R = 1024 * ceil(n / 32768)
+};
+
+// Group, job and tile within the job of one tile of a launch.
+struct TilePlace {
+    int gi;
+    uint32_t job;
+    uint32_t tile;
+};
+
+// The group of tile t: the last group whose first tile is at most t
+// (first_tiles[i] = groups[i].first_tile, ascending from 0).
+KVSZP_PLAN_FN int group_of_tile(const uint32_t* first_tiles, int num_groups, uint32_t t) {
+    int gi = 0;
+    for (int i = 1; i < num_groups; ++i)
+        if (t >= first_tiles[i]) gi = i;
+    return gi;
+}
+
+// Tile t's place, its group found in first_tiles.
+KVSZP_PLAN_FN TilePlace place_tile(const Group* groups, const uint32_t* first_tiles,
+                                   int num_groups, uint32_t t) {
+    TilePlace c;
+    c.gi = KVSZP_UNIFORM(group_of_tile(first_tiles, num_groups, t));
+    const Group& g = groups[c.gi];
+    const uint32_t local = t - g.first_tile;
+    const uint32_t jig = KVSZP_UNIFORM(local / g.tiles_per_job);
+    c.tile = local - jig * g.tiles_per_job;
+    c.job = g.first_job + jig;
+    return c;
+}
+
+// First tile of the persistent decoder's workgroup b out of G when tiles
+// are weighed by group: each tile of group g weighs tile_weight[g],
+// weight_before[g] is the weight of the tiles before the group and
+// total_weight that of all tiles (0: equal tile counts).  Run b starts
+// where the cumulative weight reaches b/G of the total (rounded up):
+// nondecreasing in b, 0 at b = 0 and total_tiles at b = G, so the runs
+// tile [0, total_tiles) exactly.
+KVSZP_PLAN_FN uint32_t weighted_run_start(const Group* groups, int num_groups,
+                                          uint32_t total_tiles, uint64_t total_weight,
+                                          const uint64_t* weight_before,
+                                          const uint32_t* tile_weight, uint32_t b,
+                                          uint32_t G) {
+    if (total_weight == 0) return (uint32_t)((uint64_t)b * total_tiles / G);
+    if (b >= G) return total_tiles;
+    const uint64_t target = (uint64_t)b * total_weight / G;
+    int g = 0;
+    for (int k = 1; k < num_groups; ++k)
+        if (weight_before[k] <= target) g = k;
+    const uint32_t first = groups[g].first_tile;
+    const uint32_t tiles =
+        (g + 1 < num_groups ? groups[g + 1].first_tile : total_tiles) - first;
+    const uint64_t w = tile_weight[g];
+    const uint64_t i = (target - weight_before[g] + w - 1) / w;
+    return first + (uint32_t)(i < tiles ? i : tiles);
+}
+
+// ---- host: building and checking a plan ------------------------------------
+
+// Header bytes of a segment of n values: one rate byte per block, for whole
+// 32768-value units (rate_offset, cuszp_batched_fixed.cu:165).
+inline uint32_t header_bytes_of(uint64_t n) {
+    return (uint32_t)((n + kRefTileElems - 1) / kRefTileElems *
+                      (kRefTileElems / kBlockElems));
+}
+
+inline uint32_t tiles_per_job_of(uint64_t n) {
+    return (uint32_t)((n + kTileElems - 1) / kTileElems);
+}
+
+// One group of a call as the caller describes it: n values per job (layer
+// map `layers` selecting `sel` of `src` layers of `epl` values, or
+// contiguous), `jobs` requests.
+struct GroupSpec {
+    uint64_t n;
+    const int64_t* layers;
+    uint64_t sel, src, epl;
+    uint32_t jobs;
+};
+
+// One launch's share of a call: groups [g0, g1) of the call's specs, with
+// job numbers global to the call and tile numbers local to the launch.
+struct Chunk {
+    size_t g0, g1;
+    uint64_t tiles;
+    uint32_t max_tiles_per_job;
+    bool whole_blocks;  // every block whole and inside one layer
+};
+
+// Splits `specs` into launches of at most kMaxGroups groups (the group
+// records travel as kernel arguments).  The reference takes any number of
+// groups (cuszp_wrapper.cpp:683-868, one launch per group).
+inline std::vector<Chunk> split_chunks(const std::vector<GroupSpec>& specs) {
+    std::vector<Chunk> chunks;
+    for (size_t g0 = 0; g0 < specs.size(); g0 += kMaxGroups) {
+        Chunk ch{g0, std::min(specs.size(), g0 + (size_t)kMaxGroups), 0, 0, true};
+        for (size_t gi = ch.g0; gi < ch.g1; ++gi) {
+            const GroupSpec& s = specs[gi];
+            const uint32_t tpj = tiles_per_job_of(s.n);
+            ch.tiles += (uint64_t)tpj * s.jobs;
+            ch.max_tiles_per_job = std::max(ch.max_tiles_per_job, tpj);
+            if ((s.n % kBlockElems) != 0 || (s.layers && (s.epl % kBlockElems) != 0))
+                ch.whole_blocks = false;
+        }
+        chunks.push_back(ch);
+    }
+    return chunks;
+}
+
+// Group records of one chunk; `first_job` is the call-wide job number of
+// the chunk's first request.  Returns the number of groups.
+inline int fill_groups(Group* groups, const std::vector<GroupSpec>& specs, const Chunk& ch,
+                       size_t first_job) {
+    uint64_t tiles = 0;
+    size_t job = first_job;
+    for (size_t gi = ch.g0; gi < ch.g1; ++gi) {
+        const GroupSpec& s = specs[gi];
+        Group& g = groups[gi - ch.g0];
+        g.n = s.n;
+        g.layers = s.layers;
+        g.selected_layers = s.sel;
+        g.source_layers = s.src;
+        g.elements_per_layer = s.epl;
+        g.first_job = (uint32_t)job;
+        g.first_tile = (uint32_t)tiles;
+        g.tiles_per_job = tiles_per_job_of(s.n);
+        g.header_bytes = header_bytes_of(s.n);
+        tiles += (uint64_t)g.tiles_per_job * s.jobs;
+        job += s.jobs;
+    }
+    return (int)(ch.g1 - ch.g0);
+}
+
+// The plan every tile loop indexes by: groups in launch order from tile 0,
+// each a whole number (at least one) of jobs numbered on from the previous
+// group's, together exactly `total_tiles`, all of them among the
+// `table_jobs` job records the kernel can read; and a grid of at least one
+// workgroup and, for the persistent kernels (a workgroup's first tile is its
+// own index), at most `total_tiles`.  The launchers check it before every
+// launch, so that no kernel indexes job records, layer maps or look-back
+// words past a plan that does not add up.
+inline bool tile_plan_ok(const Group* groups, int num_groups, uint32_t total_tiles,
+                         uint32_t grid, bool persistent, uint32_t table_jobs) {
+    if (num_groups < 1 || num_groups > kMaxGroups || total_tiles == 0 || grid == 0) return false;
+    if (persistent && grid > total_tiles) return false;
+    if (groups[0].first_tile != 0) return false;
+    for (int i = 0; i < num_groups; ++i) {
+        const Group& g = groups[i];
+        const uint32_t end = i + 1 < num_groups ? groups[i + 1].first_tile : total_tiles;
+        if (end <= g.first_tile || g.tiles_per_job == 0 || g.n == 0) return false;
+        if (tiles_per_job_of(g.n) != g.tiles_per_job) return false;
+        const uint32_t tiles = end - g.first_tile;
+        if (tiles % g.tiles_per_job != 0) return false;
+        const uint64_t jobs_end = (uint64_t)g.first_job + tiles / g.tiles_per_job;
+        if (jobs_end > table_jobs) return false;
+        if (i + 1 < num_groups && groups[i + 1].first_job != jobs_end) return false;
+    }
+    return true;
+}
+
+// Per-group tile weights of the persistent decoder (weighted_run_start):
+// a tile of group g weighs its BF16 output plus the group's average payload
+// per tile, from the stream sizes of the chunk's jobs (sizes[j] for the
+// call-wide job j, at least the group's header).  Returns total_weight.
+inline uint64_t group_tile_weights(const Group* groups, int num_groups,
+                                   const std::vector<GroupSpec>& specs, const Chunk& ch,
+                                   const uint64_t* sizes, uint64_t* weight_before,
+                                   uint32_t* tile_weight) {
+    uint64_t before = 0;
+    size_t j = groups[0].first_job;
+    for (int k = 0; k < num_groups; ++k) {
+        const GroupSpec& spec = specs[ch.g0 + (size_t)k];
+        const Group& g = groups[k];
+        uint64_t payload = 0;
+        for (uint32_t i = 0; i < spec.jobs; ++i, ++j) payload += sizes[j] - g.header_bytes;
+        const uint64_t tiles = (uint64_t)g.tiles_per_job * spec.jobs;
+        // Callers reject empty groups; the guard keeps the division defined.
+        const uint64_t w = tiles ? (2 * spec.n * spec.jobs + payload + tiles / 2) / tiles : 1;
+        tile_weight[k] = (uint32_t)std::max<uint64_t>(w, 1);
+        weight_before[k] = before;
+        before += tiles * tile_weight[k];
+    }
+    return before;
+}
+
+// Run starts of the persistent decoder balanced job by job, for a call that
+// is one launch: each job weighs its BF16 output plus its payload, spread
+// evenly over its tiles; run b starts where the cumulative weight reaches
+// b/grid of the total.  grid + 1 entries, nondecreasing, from 0 to the
+// launch's tile count.
+inline std::vector<uint32_t> job_balanced_runs(const std::vector<GroupSpec>& specs,
+                                               const uint64_t* sizes, size_t batch,
+                                               uint64_t total_tiles, uint32_t grid) {
+    std::vector<uint64_t> bytes(batch);
+    std::vector<uint32_t> tiles_of(batch);
+    uint64_t total = 0;
+    size_t j = 0;
+    for (const GroupSpec& spec : specs) {
+        const uint32_t R = header_bytes_of(spec.n);
+        const uint32_t tpj = tiles_per_job_of(spec.n);
+        for (uint32_t k = 0; k < spec.jobs; ++k, ++j) {
+            bytes[j] = 2 * spec.n + (sizes[j] - R);
+            tiles_of[j] = tpj;
+            total += bytes[j];
+        }
+    }
+    std::vector<uint32_t> runs((size_t)grid + 1);
+    size_t jj = 0;
+    uint64_t before = 0;
+    uint64_t tile_before = 0;
+    for (uint32_t b = 0; b < grid; ++b) {
+        const uint64_t target = (uint64_t)((unsigned __int128)b * total / grid);
+        while (jj < batch && before + bytes[jj] <= target) {
+            before += bytes[jj];
+            tile_before += tiles_of[jj];
+            ++jj;
+        }
+        if (jj == batch) {
+            runs[b] = (uint32_t)total_tiles;
+        } else {
+            const uint64_t i = (uint64_t)(((unsigned __int128)(target - before) * tiles_of[jj] +
+                                           bytes[jj] - 1) / bytes[jj]);
+            runs[b] = (uint32_t)(tile_before + std::min<uint64_t>(i, tiles_of[jj]));
+        }
+    }
+    runs[grid] = (uint32_t)total_tiles;
+    return runs;
+}
+
+}  // namespace kvszp
+
+#endif  // KVSZP_PLAN_H

@@ -43,3 +43,18 @@ def test_whole_field_quantizer_matches_oracle(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "mismatches=0" in out.stdout
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_tile_plan_walk(tmp_path):
+    """Every tile of random calls placed by the kernels' lookup, with bounds
+    checks, on plans built by the C-ABI's own functions (csrc/kvszp_plan.h);
+    the launch check accepts them and rejects plans that do not add up."""
+    exe = tmp_path / "tile_plan_test"
+    subprocess.run(
+        ["g++", "-O2", "-std=c++17", "-I", os.path.join(PKG, "csrc"),
+         os.path.join(REPO, "tests", "host", "tile_plan_test.cpp"), "-o", str(exe)],
+        check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "mismatches=0" in out.stdout
