@@ -89,23 +89,32 @@ KVSZP_PLAN_FN TilePlace place_tile(const Group* groups, const uint32_t* first_ti
 // where the cumulative weight reaches b/G of the total (rounded up):
 // nondecreasing in b, 0 at b = 0 and total_tiles at b = G, so the runs
 // tile [0, total_tiles) exactly.
+//
+// The quotients are taken in double precision: every wave works out two run
+// starts before its first tile, and a 64-bit integer division is a long
+// scalar sequence (four per wave held back the first tiles of the
+// workgroups issued last).  Rounding is monotone, so the starts stay
+// nondecreasing whatever the sizes (the products are exact anyway for a
+// resident grid, b < 2^12, and total_weight < 2^40: at most 2^24 tiles of
+// weight below 2^16), and a workgroup and its successor compute the same
+// value for the boundary they share.
 KVSZP_PLAN_FN uint32_t weighted_run_start(const Group* groups, int num_groups,
                                           uint32_t total_tiles, uint64_t total_weight,
                                           const uint64_t* weight_before,
                                           const uint32_t* tile_weight, uint32_t b,
                                           uint32_t G) {
-    if (total_weight == 0) return (uint32_t)((uint64_t)b * total_tiles / G);
     if (b >= G) return total_tiles;
-    const uint64_t target = (uint64_t)b * total_weight / G;
+    if (total_weight == 0)
+        return (uint32_t)((double)b * (double)total_tiles / (double)G);
+    const uint64_t target = (uint64_t)((double)b * (double)total_weight / (double)G);
     int g = 0;
     for (int k = 1; k < num_groups; ++k)
         if (weight_before[k] <= target) g = k;
     const uint32_t first = groups[g].first_tile;
     const uint32_t tiles =
         (g + 1 < num_groups ? groups[g + 1].first_tile : total_tiles) - first;
-    const uint64_t w = tile_weight[g];
-    const uint64_t i = (target - weight_before[g] + w - 1) / w;
-    return first + (uint32_t)(i < tiles ? i : tiles);
+    const double i = __builtin_ceil((double)(target - weight_before[g]) / (double)tile_weight[g]);
+    return first + (i < (double)tiles ? (uint32_t)i : tiles);
 }
 
 // ---- host: building and checking a plan ------------------------------------
