@@ -71,7 +71,9 @@ sys.path.insert(0, PKG)
 
 METRIC = "KV compress/decompress GB/s (BF16 in), % of HBM peak, ratio at eb=1e-4"
 HBM_PEAK_GBPS = 8000.0
-KERNELS_SRC = os.path.join(PKG, "csrc", "kvszp_kernels.hip")
+# The device code: the kernels and the headers they include.
+KERNELS_SRC = [os.path.join(PKG, "csrc", f) for f in
+               ("kvszp_kernels.hip", "kvszp_internal.h", "kvszp_plan.h", "kvszp_bits.h")]
 
 
 def traffic_file(config: int) -> str:
@@ -84,8 +86,11 @@ def log(msg: str) -> None:
 
 
 def kernels_sha() -> str:
-    with open(KERNELS_SRC, "rb") as f:
-        return hashlib.sha256(f.read()).hexdigest()[:16]
+    h = hashlib.sha256()
+    for path in KERNELS_SRC:
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
 
 
 # ---- workloads -------------------------------------------------------------------
