@@ -1077,6 +1077,7 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
     g.first_tile = 0;
     g.tiles_per_job = tiles_per_job;
     g.header_bytes = header_bytes_of(n);
+    set_group_divisors(g);
     p.num_groups = 1;
     // After a recent give-up, the schedule that needs no residency at once.
     const bool schedule_safe = c->safe_left > 0;

@@ -1280,9 +1280,9 @@ __device__ __forceinline__ uint64_t enc_block_source(const Group& g, uint32_t ti
     if (g.layers == nullptr) return E + (uint32_t)lane * kBlockElems;
     const uint32_t epl = (uint32_t)g.elements_per_layer;
     const uint32_t per_prefix = (uint32_t)g.selected_layers * epl;
-    const uint32_t pre = E / per_prefix;
+    const uint32_t pre = divide(E, g.prefix_div);
     const uint32_t within = E - pre * per_prefix;
-    const uint32_t layer = within / epl;
+    const uint32_t layer = divide(within, g.layer_div);
     const uint32_t inner = within - layer * epl;
     if (inner + kRun <= epl) {
         int64_t l = load_const(g.layers, layer);
@@ -1346,9 +1346,9 @@ __device__ __forceinline__ WaveSource wave_source(const CompressParams& p, const
     }
     const uint32_t epl = (uint32_t)g.elements_per_layer;
     const uint32_t per_prefix = (uint32_t)g.selected_layers * epl;
-    const uint32_t pre = E / per_prefix;
+    const uint32_t pre = divide(E, g.prefix_div);
     const uint32_t within = E - pre * per_prefix;
-    const uint32_t layer = within / epl;
+    const uint32_t layer = divide(within, g.layer_div);
     const uint32_t inner = within - layer * epl;
     const int64_t l = load_const(g.layers, layer);
     s.base = (inner + kRun <= epl && l >= 0 && (uint64_t)l < g.source_layers)
@@ -2455,9 +2455,9 @@ __device__ __forceinline__ uint16_t* wave_run_dst(const DecompressParams& p,
     } else {
         const uint32_t epl = (uint32_t)g.elements_per_layer;
         const uint32_t per_prefix = (uint32_t)g.selected_layers * epl;
-        const uint32_t pre = E / per_prefix;
+        const uint32_t pre = divide(E, g.prefix_div);
         const uint32_t within = E - pre * per_prefix;
-        const uint32_t layer = within / epl;
+        const uint32_t layer = divide(within, g.layer_div);
         const uint32_t inner = within - layer * epl;
         if (inner + kRun > epl) return nullptr;
         const int64_t l = load_const(g.layers, layer);

@@ -41,6 +41,24 @@ constexpr int kTileElems = kTileBlocks * kBlockElems;
 constexpr int kRefTileElems = 32768;                // header granularity
 constexpr int kMaxGroups = 16;
 
+// Division by a launch constant d (1 <= d < 2^32) of an index below 2^29
+// (segments hold at most 2^29 values, so every element, tile and job index
+// of a launch qualifies) as one multiply and one shift: with
+// l = ceil(log2 d) and m = ceil(2^(29+l) / d), floor(n m / 2^(29+l)) =
+// floor(n / d) for every n < 2^29, because 2^(29+l) <= m d <= 2^(29+l) + 2^l
+// (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, Theorem 4.2).  The kernels divide by a job's
+// tile count and by its layer geometry on every tile; the generic 32-bit
+// division is a sequence of some twenty instructions.
+struct Divisor {
+    uint32_t mul;
+    uint32_t shift;
+};
+
+KVSZP_PLAN_FN uint32_t divide(uint32_t n, Divisor d) {
+    return (uint32_t)(((uint64_t)n * d.mul) >> d.shift);
+}
+
 struct Group {
     uint64_t n;                 // logical elements per job
     const int64_t* layers;      // device layer map, nullptr = contiguous
@@ -51,6 +69,9 @@ struct Group {
     uint32_t first_tile;
     uint32_t tiles_per_job;
     uint32_t header_bytes;      // R = 1024 * ceil(n / 32768)
+    Divisor tiles_per_job_div;  // by tiles_per_job
+    Divisor layer_div;          // by elements_per_layer (layer maps only)
+    Divisor prefix_div;         // by selected_layers * elements_per_layer (layer maps only)
 };
 
 // Group, job and tile within the job of one tile of a launch.
@@ -76,7 +97,7 @@ KVSZP_PLAN_FN TilePlace place_tile(const Group* groups, const uint32_t* first_ti
     c.gi = KVSZP_UNIFORM(group_of_tile(first_tiles, num_groups, t));
     const Group& g = groups[c.gi];
     const uint32_t local = t - g.first_tile;
-    const uint32_t jig = KVSZP_UNIFORM(local / g.tiles_per_job);
+    const uint32_t jig = KVSZP_UNIFORM(divide(local, g.tiles_per_job_div));
     c.tile = local - jig * g.tiles_per_job;
     c.job = g.first_job + jig;
     return c;
@@ -128,6 +149,26 @@ inline uint32_t header_bytes_of(uint64_t n) {
 
 inline uint32_t tiles_per_job_of(uint64_t n) {
     return (uint32_t)((n + kTileElems - 1) / kTileElems);
+}
+
+// The multiplier and shift of `divide` for d (1 <= d < 2^32; 0 gives a
+// divisor that tile_plan_ok rejects).
+inline Divisor divisor_of(uint32_t d) {
+    if (d == 0) return Divisor{0, 0};
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    const uint32_t shift = 29 + l;
+    return Divisor{(uint32_t)(((1ull << shift) + d - 1) / d), shift};
+}
+
+inline bool same_divisor(Divisor a, Divisor b) { return a.mul == b.mul && a.shift == b.shift; }
+
+// The divisors of a group's record from its geometry.
+inline void set_group_divisors(Group& g) {
+    g.tiles_per_job_div = divisor_of(g.tiles_per_job);
+    g.layer_div = g.layers ? divisor_of((uint32_t)g.elements_per_layer) : Divisor{0, 0};
+    g.prefix_div = g.layers ? divisor_of((uint32_t)(g.selected_layers * g.elements_per_layer))
+                            : Divisor{0, 0};
 }
 
 // One group of a call as the caller describes it: n values per job (layer
@@ -187,6 +228,7 @@ inline int fill_groups(Group* groups, const std::vector<GroupSpec>& specs, const
         g.first_tile = (uint32_t)tiles;
         g.tiles_per_job = tiles_per_job_of(s.n);
         g.header_bytes = header_bytes_of(s.n);
+        set_group_divisors(g);
         tiles += (uint64_t)g.tiles_per_job * s.jobs;
         job += s.jobs;
     }
@@ -211,6 +253,14 @@ inline bool tile_plan_ok(const Group* groups, int num_groups, uint32_t total_til
         const uint32_t end = i + 1 < num_groups ? groups[i + 1].first_tile : total_tiles;
         if (end <= g.first_tile || g.tiles_per_job == 0 || g.n == 0) return false;
         if (tiles_per_job_of(g.n) != g.tiles_per_job) return false;
+        if (!same_divisor(g.tiles_per_job_div, divisor_of(g.tiles_per_job))) return false;
+        if (g.layers &&
+            (g.elements_per_layer == 0 ||
+             g.selected_layers * g.elements_per_layer > 0xFFFFFFFFull ||
+             !same_divisor(g.layer_div, divisor_of((uint32_t)g.elements_per_layer)) ||
+             !same_divisor(g.prefix_div,
+                           divisor_of((uint32_t)(g.selected_layers * g.elements_per_layer)))))
+            return false;
         const uint32_t tiles = end - g.first_tile;
         if (tiles % g.tiles_per_job != 0) return false;
         const uint64_t jobs_end = (uint64_t)g.first_job + tiles / g.tiles_per_job;

@@ -177,7 +177,16 @@ int main() {
             uint64_t n = kSizes[rng() % (sizeof(kSizes) / sizeof(kSizes[0]))];
             if (rng() % 4 == 0) n = 1 + rng() % (1u << 21);
             const uint32_t jobs = 1 + (uint32_t)(rng() % (rng() % 8 == 0 ? 300 : 12));
-            specs.push_back(GroupSpec{n, nullptr, 0, 0, 0, jobs});
+            if (rng() % 3 == 0) {
+                // a layer-mapped group: sel of src layers of epl values, n = prefix x sel x epl
+                static const int64_t kMap[1] = {0};
+                const uint64_t epl = 32u * (1u + rng() % 512u), sel = 1u + rng() % 8u;
+                const uint64_t prefix = 1u + rng() % 2u;
+                n = prefix * sel * epl;
+                specs.push_back(GroupSpec{n, kMap, sel, sel + rng() % 4u, epl, jobs});
+            } else {
+                specs.push_back(GroupSpec{n, nullptr, 0, 0, 0, jobs});
+            }
             tiles += (uint64_t)tiles_per_job_of(n) * jobs;
         }
         if (tiles > 400000) continue;
@@ -210,6 +219,45 @@ int main() {
         }
     }
 
+    // The kernels' division by a launch constant, against the hardware
+    // division: every divisor class (1, powers of two and their neighbours,
+    // the library's tile counts and layer sizes, random ones up to 2^32 - 1)
+    // at the ends of the index range and at random indices below 2^29.
+    {
+        std::vector<uint32_t> ds{1u, 2u, 3u, 5u, 6u, 7u, 21u, 28u, 128u, 4096u, 28672u, 86016u,
+                                 (1u << 29) - 1u, 1u << 29, (1u << 29) + 1u, 0xFFFFFFFFu,
+                                 0xFFFFFFFEu, 0x80000000u, 0x80000001u};
+        for (int k = 1; k < 32; ++k) {
+            ds.push_back(1u << k);
+            ds.push_back((1u << k) - 1u);
+            ds.push_back((1u << k) + 1u);
+        }
+        for (int i = 0; i < 2000; ++i) ds.push_back(1u + (uint32_t)(rng() % 0xFFFFFFFFull));
+        for (int i = 0; i < 2000; ++i) ds.push_back(1u + (uint32_t)(rng() % 100000u));
+        long checked = 0;
+        for (uint32_t d : ds) {
+            const Divisor dv = divisor_of(d);
+            std::vector<uint32_t> ns{0u, 1u, d - 1u, d, d + 1u, (1u << 29) - 1u, (1u << 29) - 2u};
+            for (int i = 0; i < 200; ++i) ns.push_back((uint32_t)(rng() % (1u << 29)));
+            for (uint32_t m = 1; m < 64 && (uint64_t)m * d < (1u << 29); ++m) {
+                ns.push_back(m * d - 1u);
+                ns.push_back(m * d);
+            }
+            for (uint32_t n : ns) {
+                if (n >= (1u << 29)) continue;
+                CHECK(divide(n, dv) == n / d, "%u / %u: %u", n, d, divide(n, dv));
+                ++checked;
+            }
+        }
+        // every index below 2^16 for small divisors
+        for (uint32_t d = 1; d < 300; ++d) {
+            const Divisor dv = divisor_of(d);
+            for (uint32_t n = 0; n < (1u << 16); ++n) CHECK(divide(n, dv) == n / d, "%u / %u", n, d);
+            checked += 1 << 16;
+        }
+        std::printf("divisions=%ld\n", checked);
+    }
+
     // Plans that do not add up are rejected (planted on the host).
     {
         std::vector<GroupSpec> specs{GroupSpec{20000, nullptr, 0, 0, 0, 4},
@@ -230,6 +278,8 @@ int main() {
         reset(); CHECK(!tile_plan_ok(g, 0, 17, 17, false, 9), "no groups accepted");
         reset(); CHECK(!tile_plan_ok(g, ng, 17, 0, false, 9), "empty grid accepted");
         reset(); CHECK(!tile_plan_ok(g, kMaxGroups + 1, 17, 17, false, 9), "too many groups accepted");
+        reset(); g[1].tiles_per_job_div.mul += 1; CHECK(!tile_plan_ok(g, ng, 17, 17, false, 9), "wrong divisor accepted");
+        reset(); g[0].tiles_per_job_div = Divisor{0, 0}; CHECK(!tile_plan_ok(g, ng, 17, 17, false, 9), "missing divisor accepted");
     }
 
     std::printf("launches=%ld tiles=%ld mismatches=%ld\n", launches, tiles_checked, g_bad);
