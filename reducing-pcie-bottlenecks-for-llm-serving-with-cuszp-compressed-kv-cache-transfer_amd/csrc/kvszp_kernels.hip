@@ -1648,6 +1648,39 @@ __device__ __forceinline__ void copy_payload(uint32_t* dst, uint32_t words,
     __asm__ volatile("" ::: "memory");  // before the words are reused
 }
 
+// Writes the payload of a wave whose blocks all hold one value, quantized to
+// q != 0 (`words` words to `dst`, 4-byte aligned): every block is the same
+// rate + 1 words (cu:302-358), the sign word and planes 0 .. rate - 1 of |q|,
+// each word all ones or all zeros.  Lane l writes words 4l .. 4l + 3 of every
+// 256-word chunk, as copy_payload does, with no staging.
+__device__ __forceinline__ void fill_uniform_payload(uint32_t* dst, uint32_t words,
+                                                     int32_t q, int lane) {
+    const uint32_t m = magnitude(q);
+    const uint32_t period = 33u - (uint32_t)__builtin_clz(m);  // rate + 1
+    const uint32_t sign = q < 0 ? ~0u : 0u;
+    g_u32* d = to_global(dst);
+    const uint32_t quads = words >> 2;
+    for (uint32_t qd = (uint32_t)lane; qd < quads; qd += 64u) {
+        uint32_t j = (4u * qd) % period, w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[i] = j == 0 ? sign : 0u - ((m >> (j - 1u)) & 1u);
+            j = j + 1u == period ? 0u : j + 1u;
+        }
+        u32x4 v;
+        v.x = w[0];
+        v.y = w[1];
+        v.z = w[2];
+        v.w = w[3];
+        *(g_u32x4_a4*)(d + 4u * qd) = v;
+    }
+    const uint32_t tail = 4u * quads + (uint32_t)lane;
+    if (tail < words) {
+        const uint32_t j = tail % period;
+        d[tail] = j == 0 ? sign : 0u - ((m >> (j - 1u)) & 1u);
+    }
+}
+
 // Words 16 .. count - 1 of a block (rates above 15), exactly (no slot past
 // `count` is written: the low words of later blocks are already in place).
 __device__ __forceinline__ void stage_high_words(const uint32_t* P, uint32_t count,
@@ -1711,7 +1744,9 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
     __shared__ uint32_t s_gfirst[kMaxGroups];
     __shared__ uint8_t s_rate[2][kTileBlocks];
     __shared__ PendingTile s_pend[2];  // by the parity of the tile it holds
-    __shared__ uint32_t s_pwave[kEncWaves][2];  // staged: wave offset, words
+    // staged: wave offset, words (bit 31: the payload is one block repeated,
+    // not staged), that block's q
+    __shared__ uint32_t s_pwave[kEncWaves][3];
     __shared__ uint32_t s_abort;       // a bounded wait of this launch gave up
     __shared__ __attribute__((aligned(16))) uint32_t s_stage[kEncWaves][kEncStageWords];
 
@@ -1957,9 +1992,14 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         if (pending) {
             const PendingTile& q = s_pend[parity ^ 1u];
             const uint32_t woff = s_pwave[wave][0], words = s_pwave[wave][1];
-            if (words)
-                copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[parity] + woff),
-                             words, &s_stage[wave][0], lane);
+            if (words) {
+                uint32_t* dst = reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[parity] + woff);
+                if (words >> 31)
+                    fill_uniform_payload(dst, words & 0x7FFFFFFFu, (int32_t)s_pwave[wave][2],
+                                         lane);
+                else
+                    copy_payload(dst, words, &s_stage[wave][0], lane);
+            }
         }
 
         // e. rows (cu:180-231) and staging (cu:302-358: sign word, then
@@ -1969,15 +2009,27 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         // whose transpose gives words 0..15 in stream order, and for rates
         // above 15 the high fields |q| >> 15 (words 16..31), staged exactly.
         // A wave whose payload would not fit the staging words (rates far
-        // above 15 throughout, e.g. a constant page under a relative bound)
-        // stages nothing and marks its job; the host encodes the marked jobs
-        // again with the one-workgroup-per-tile kernel.  Sizes, bounds and
-        // every other job of this launch come out normally.
+        // above 15 throughout) stages nothing.  When all its blocks hold one
+        // value (every block's min and max keys are the same key: no NaN, no
+        // absent block), as on a constant page under a relative bound, its
+        // payload is that value's block repeated, written at d. from q alone.
+        // Otherwise it marks its job; the host encodes the marked jobs again
+        // with the one-workgroup-per-tile kernel.  Sizes, bounds and every
+        // other job of this launch come out normally.
         // Only the first wave to mark a job writes host memory: the marks of
         // every wave of a saturated page would be a stream of small writes
         // across the link, most of them to one word.
         const bool overflow = (wave_bytes >> 2) + 16u > (uint32_t)kEncStageWords;
+        bool uniform = false;
         if (overflow) {
+            const uint32_t ukey = __builtin_amdgcn_readfirstlane(keys0);
+            uniform = (ukey >> 16) == (ukey & 0xFFFFu) &&
+                      __ballot(keys0 != ukey || keys1 != ukey) == 0ull;
+            if (uniform && lane == 0)
+                s_pwave[wave][2] =
+                    (uint32_t)quantize<kQuant>(key_value(ukey & 0xFFFFu), recip);
+        }
+        if (overflow && !uniform) {
             if (lane == 0 &&
                 __hip_atomic_exchange(&p.job_flags[cur.job], p.epoch, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT) != p.epoch) {
@@ -1986,7 +2038,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
                 __hip_atomic_store(&p.host_ctl[kHostOverflow], p.seq, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_SYSTEM);
             }
-        } else {
+        } else if (!overflow) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 uint32_t (&X)[16] = h ? X1 : X0;
@@ -2016,7 +2068,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         }
         if (lane == 0) {
             s_pwave[wave][0] = wave_off;
-            s_pwave[wave][1] = overflow ? 0u : wave_bytes >> 2;
+            s_pwave[wave][1] = !overflow ? wave_bytes >> 2
+                               : uniform ? (wave_bytes >> 2) | 0x80000000u : 0u;
         }
         // Written by the wave that reads it first (wave 1's look-back in the
         // next iteration, or the flush below); wave 0 reads it only after the
@@ -2069,9 +2122,13 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         if (s_abort) return;
         const PendingTile& q = s_pend[parity];
         const uint32_t woff = s_pwave[wave][0], words = s_pwave[wave][1];
-        if (words)
-            copy_payload(reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[2] + woff),
-                         words, &s_stage[wave][0], lane);
+        if (words) {
+            uint32_t* dst = reinterpret_cast<uint32_t*>(q.out + q.R + s_prefix[2] + woff);
+            if (words >> 31)
+                fill_uniform_payload(dst, words & 0x7FFFFFFFu, (int32_t)s_pwave[wave][2], lane);
+            else
+                copy_payload(dst, words, &s_stage[wave][0], lane);
+        }
     }
 }
 
