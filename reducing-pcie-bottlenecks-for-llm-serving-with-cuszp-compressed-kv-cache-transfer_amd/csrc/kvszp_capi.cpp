@@ -85,6 +85,10 @@ struct kvszp_ctx {
     int rate0 = KVSZP_RATE0_ZERO;
     uint32_t fused_tile_limit = 0;
     bool use_tickets = false;  // KVSZP_TICKETS=1: ticket-ordered tiles
+    // Job tables of the persistent kernels that fit an ArgTable travel in
+    // the kernel arguments instead of a table copy on the stream
+    // (KVSZP_ARG_TABLES=0 turns that off).
+    int arg_tables = 3;  // bit 0: stores, bit 1: restores
     // Time bound of the encoders' cross-workgroup waits, in steady-clock
     // ticks (KVSZP_WAIT_US, default 200 us), and how many calls were encoded
     // again after a launch gave up or overflowed.
@@ -474,17 +478,25 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         (rc = ensure_host_results(c, batch * 12)))
         return rc;
     const uint32_t seq = ++c->seq;
-    // Small calls pass the job table in the kernel arguments (no upload).
+    // Small calls pass the job table in the kernel arguments (no upload), and
+    // so do persistent-encoder launches whose table fits an ArgTable.  The
+    // table is uploaded, once, for every other launch: from the start, or
+    // when a launch is encoded again with the schedule that needs no
+    // residency.
     const bool inline_jobs = batch <= (size_t)kInlineJobs;
-    if (!inline_jobs) {
-        rc = upload_tables(c, jobs.data(), batch * sizeof(CompressJob), seq, stream);
-        if (rc) return rc;
-    }
+    const size_t table_bytes = batch * sizeof(CompressJob);
+    const bool arg_table = !inline_jobs && (c->arg_tables & 1) && table_bytes <= kArgTableBytes;
+    bool uploaded = false;
+    auto need_table = [&]() -> int {
+        if (inline_jobs || uploaded) return KVSZP_OK;
+        uploaded = true;
+        return upload_tables(c, jobs.data(), table_bytes, seq, stream);
+    };
+    if (!arg_table && (rc = need_table())) return rc;
 
     uint32_t* host_sizes = reinterpret_cast<uint32_t*>(c->host_results);
     float* host_bounds = reinterpret_cast<float*>(host_sizes + batch);
     uint32_t* host_redo = host_sizes + 2 * batch;
-    const CompressJob* djobs = reinterpret_cast<const CompressJob*>(c->tables.ptr);
 
     // One launch per chunk (normally one); all share the call's sequence
     // number and table, each has its own epoch (the look-back and min/max
@@ -508,6 +520,21 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         if (relative)
             bound_mode = (!safe && !f32 && ch.max_tiles_per_job <= c->fused_tile_limit)
                              ? kBoundFused : kBoundPrepass;
+        // Persistent encoder (whole, aligned, single-layer blocks only); its
+        // waits are cycle-free while a job's tiles number at most the grid
+        // (half of it here, for margin) and all its workgroups are resident.
+        const bool persistent = !safe && !f32 && bound_mode != kBoundPrepass &&
+                                c->pipelined_grid != 0 && ch.whole_blocks && aligned16 &&
+                                ch.max_tiles_per_job <= c->pipelined_grid / 2;
+        const bool use_arg = persistent && arg_table;
+        if (!use_arg) {
+            const int r = need_table();
+            if (r) return r;
+        }
+        // The uploaded table, read only after the upload (which may have
+        // grown the buffer); ArgTable and inline launches read no table.
+        const CompressJob* djobs =
+            uploaded ? reinterpret_cast<const CompressJob*>(c->tables.ptr) : nullptr;
         uint32_t epoch;
         int r = next_epoch(c, stream, &epoch);
         if (r) return r;
@@ -560,22 +587,18 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         p.aligned16 = aligned16 ? 1 : 0;
         p.input_f32 = f32 ? 1 : 0;
         p.mode = f32 ? mode : kModeFixed;
-        const bool persistent = !safe && !f32 && bound_mode != kBoundPrepass &&
-                                c->pipelined_grid != 0 && ch.whole_blocks && aligned16 &&
-                                ch.max_tiles_per_job <= c->pipelined_grid / 2;
+        if (use_arg) p.jobs_inline = 2;
         if (persistent || bound_mode == kBoundFused) {
             p.abort_word = abort_word(c);
             p.wait_ticks = c->wait_ticks;
         }
         redo_candidate[k] = p.abort_word != nullptr;
         if (persistent) {
-            // Persistent encoder (whole, aligned, single-layer blocks only); its
-            // waits are cycle-free while a job's tiles number at most the grid
-            // (half of it here, for margin) and all its workgroups are resident.
             p.ticket = nullptr;
             const uint32_t grid = (uint32_t)std::min<uint64_t>(ch.tiles, c->pipelined_grid);
             e = launch_compress_pipelined(p, grid, stream, timing_start(c, rec),
-                                          timing_stop(c, rec));
+                                          timing_stop(c, rec), use_arg ? jobs.data() : nullptr,
+                                          use_arg ? table_bytes : 0);
         } else {
             e = launch_compress(p, stream,
                                 bound_mode == kBoundPrepass ? nullptr : timing_start(c, rec),
@@ -752,10 +775,16 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     if ((rc = ensure(c->tile_state, max_tiles * 8, true, stream))) return rc;
     const uint32_t seq = ++c->seq;
     // Small calls without a destination table or run starts pass their job
-    // table in the kernel arguments (no upload).
+    // table in the kernel arguments (no upload), and so does a persistent
+    // launch whose job table (no destination table, no run starts) fits an
+    // ArgTable.
     const bool inline_jobs =
         batch <= (size_t)kInlineJobs && dest_table.empty() && runs.empty();
-    if (!inline_jobs && (rc = upload_tables(c, table.data(), table.size(), seq, stream)))
+    const size_t job_bytes = batch * sizeof(DecompressJob);
+    const bool arg_table = !inline_jobs && (c->arg_tables & 2) && persistent &&
+                           dest_table.empty() && runs.empty() && job_bytes <= kArgTableBytes;
+    if (!inline_jobs && !arg_table &&
+        (rc = upload_tables(c, table.data(), table.size(), seq, stream)))
         return rc;
 
     size_t first_job = 0;
@@ -778,6 +807,8 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
         if (inline_jobs) {
             p.jobs_inline = 1;
             std::memcpy(p.inline_jobs, jobs.data(), batch * sizeof(DecompressJob));
+        } else if (arg_table) {
+            p.jobs_inline = 2;
         }
         p.dests = reinterpret_cast<uint16_t* const*>(
             reinterpret_cast<char*>(c->tables.ptr) + jobs_bytes);
@@ -810,7 +841,9 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
                 return fail(KVSZP_EINVAL, "decoder run table for %zu workgroups, launch of %u",
                             runs.size() - 1, grid);
             e = launch_decompress_persistent(p, grid, stream, timing_start(c, rec),
-                                             timing_stop(c, rec));
+                                             timing_stop(c, rec),
+                                             arg_table ? jobs.data() : nullptr,
+                                             arg_table ? job_bytes : 0);
         } else {
             e = launch_decompress(p, stream, timing_start(c, rec), timing_stop(c, rec));
         }
@@ -848,6 +881,8 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
     {
         const char* env = std::getenv("KVSZP_TICKETS");
         c->use_tickets = env && env[0] == '1';
+        const char* at = std::getenv("KVSZP_ARG_TABLES");
+        c->arg_tables = at ? std::atoi(at) & 3 : 3;
         int khz = 0;
         if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device_id) !=
                 hipSuccess || khz <= 0)

@@ -24,6 +24,19 @@ constexpr int kThreads = kTileBlocks;               // one thread per block
 // Calls of at most this many jobs pass their job table in the kernel
 // arguments (no table upload before the launch).
 constexpr int kInlineJobs = 16;
+// Job tables of up to kArgTableBytes (`jobs_inline` 2): the persistent
+// kernels' *_argtable_kernel variants take an ArgTable as a second kernel
+// argument, so the records travel with the launch, right behind the
+// parameter block at arg_table_offset<Params>() in the kernel-argument
+// segment.  The launch then needs no table copy on the stream before it.
+constexpr size_t kArgTableBytes = 14336;
+struct alignas(16) ArgTable {
+    unsigned char bytes[kArgTableBytes];
+};
+template <class Params>
+constexpr size_t arg_table_offset() {
+    return (sizeof(Params) + alignof(ArgTable) - 1) & ~(alignof(ArgTable) - 1);
+}
 constexpr uint32_t kSpinLimit = 1u << 20;           // bounded waits (~1 s)
 
 // Device-side error bits (OR-ed into the context's error word).
@@ -116,7 +129,7 @@ struct CompressParams {
     uint64_t wait_ticks;
     Group groups[kMaxGroups];
     uint32_t num_jobs;                // job records in the table (jobs or inline_jobs)
-    int jobs_inline;                  // 1: the jobs are inline_jobs, not *jobs
+    int jobs_inline;                  // 1: inline_jobs; 2: the ArgTable; 0: *jobs
     CompressJob inline_jobs[kInlineJobs];
 };
 
@@ -168,7 +181,7 @@ struct DecompressParams {
     uint32_t tile_weight[kMaxGroups];
     Group groups[kMaxGroups];
     uint32_t num_jobs;                // job records in the table (jobs or inline_jobs)
-    int jobs_inline;                  // 1: the jobs are inline_jobs, not *jobs
+    int jobs_inline;                  // 1: inline_jobs; 2: the ArgTable; 0: *jobs
     DecompressJob inline_jobs[kInlineJobs];
 };
 
@@ -220,9 +233,12 @@ hipError_t launch_fill_u64(unsigned long long* words, size_t count, hipStream_t 
 hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
                            hipEvent_t start, hipEvent_t stop);
 // Persistent encoder: `grid` workgroups (all co-resident) walk the tiles.
+// With p.jobs_inline == 2 the `table_bytes` bytes at `table` (the job
+// records) go into the kernel arguments.
 hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
                                      hipStream_t stream, hipEvent_t start,
-                                     hipEvent_t stop);
+                                     hipEvent_t stop, const void* table = nullptr,
+                                     size_t table_bytes = 0);
 hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
                          hipStream_t stream, hipEvent_t start);
 hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
@@ -231,7 +247,8 @@ hipError_t launch_decompress(const DecompressParams& p, hipStream_t stream,
 // tiles; it has no cross-workgroup waits.
 hipError_t launch_decompress_persistent(const DecompressParams& p, uint32_t grid,
                                        hipStream_t stream, hipEvent_t start,
-                                       hipEvent_t stop);
+                                       hipEvent_t stop, const void* table = nullptr,
+                                       size_t table_bytes = 0);
 int decompress_resident_workgroups(int device);
 // Maximum co-resident workgroups of an encoder kernel on this device.
 int compress_resident_workgroups(int device, bool pipelined);

@@ -32,7 +32,9 @@
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <cstring>
 #include <mutex>
+#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -64,11 +66,28 @@ __device__ __forceinline__ T load_const(const T* table, uint32_t i) {
 #endif
 }
 
+// Record i of the ArgTable behind the parameter block in the kernel-argument
+// segment (only kernels launched with an ArgTable argument get
+// jobs_inline == 2 from the host).
+template <typename T, class Params>
+__device__ __forceinline__ T arg_table_record(uint32_t i) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef const __attribute__((address_space(4))) unsigned char k_u8;
+    k_u8* k = (k_u8*)__builtin_amdgcn_kernarg_segment_ptr();
+    return ((const __attribute__((address_space(4))) T*)(k + arg_table_offset<Params>()))[i];
+#else
+    return T{};  // host pass only parses this
+#endif
+}
+
 // Job record i of a launch: from the kernel arguments for calls of at most
-// kInlineJobs jobs, else from the uploaded table (`jobs_inline` is uniform,
-// so this is a scalar branch).
+// kInlineJobs jobs or for ArgTable launches, else from the uploaded table
+// (`jobs_inline` is uniform, so these are scalar branches).
 template <class Params>
 __device__ __forceinline__ auto job_at(const Params& p, uint32_t i) {
+    typedef typename std::remove_cv<
+        typename std::remove_reference<decltype(p.inline_jobs[0])>::type>::type Job;
+    if (p.jobs_inline == 2) return arg_table_record<Job, Params>(i);
     return p.jobs_inline ? p.inline_jobs[i] : load_const(p.jobs, i);
 }
 
@@ -1733,9 +1752,7 @@ __device__ __forceinline__ void stage_high_words(const uint32_t* P, uint32_t cou
 // last microseconds; the bound is hundreds, so the mark costs nothing when
 // the device is not contended.
 template <int kQuant, bool kEarly>
-__global__ __launch_bounds__(kEncThreads)
-__attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
-    CompressParams p) {
+__device__ __forceinline__ void compress_persistent(const CompressParams& p) {
     __shared__ uint32_t s_wave[2][kEncWaves];
     __shared__ uint32_t s_min[kEncWaves], s_max[kEncWaves];
     __shared__ float s_bnd[2][2];      // by tile parity: eb, recip
@@ -1774,6 +1791,21 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         const int lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const Group& g = p.groups[cur.gi];
+        // ArgTable launches: the job records were written by the host just
+        // before the launch and sit in no cache.  Workgroups 0-7 (one on
+        // each XCD) read one word of every 64-byte line of the table before
+        // their first tile, so that the record reads of the other
+        // workgroups' later tiles hit their XCD's L2.
+        uint32_t touch0 = 0, touch1 = 0;
+        if (p.jobs_inline == 2 && blockIdx.x < 8u) {
+            const uint32_t lines = (p.num_jobs * (uint32_t)sizeof(CompressJob) + 63u) / 64u;
+            typedef const __attribute__((address_space(4))) unsigned char k_u8;
+            k_u8* k = (k_u8*)__builtin_amdgcn_kernarg_segment_ptr() +
+                      arg_table_offset<CompressParams>();
+            const uint32_t i0 = (uint32_t)tid, i1 = (uint32_t)tid + kEncThreads;
+            touch0 = *(const __attribute__((address_space(1))) uint32_t*)(k + 64u * (i0 < lines ? i0 : 0u));
+            touch1 = *(const __attribute__((address_space(1))) uint32_t*)(k + 64u * (i1 < lines ? i1 : 0u));
+        }
         load_block_regs(p, cur, g, 2 * wave, lane, D0);
         load_block_regs(p, cur, g, 2 * wave + 1, lane, D1);
         uint32_t nan0, nan1;
@@ -1786,6 +1818,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
         if (nan1) keys1 = kNanRateKeys;
         has_next = cur.t + G < p.total_tiles;
         if (has_next) nxt = tile_ctx(p, cur.t + G, s_gfirst);
+        __asm__ volatile("" ::"v"(touch0), "v"(touch1));  // older than the tile's loads
         __syncthreads();  // thread 0 has read s_min/s_max before c. rewrites them
     }
 
@@ -2130,6 +2163,20 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(
                 copy_payload(dst, words, &s_stage[wave][0], lane);
         }
     }
+}
+
+template <int kQuant, bool kEarly>
+__global__ __launch_bounds__(kEncThreads)
+__attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_kernel(CompressParams p) {
+    compress_persistent<kQuant, kEarly>(p);
+}
+
+// The same with the job records in the kernel arguments (jobs_inline == 2).
+template <int kQuant, bool kEarly>
+__global__ __launch_bounds__(kEncThreads)
+__attribute__((amdgpu_waves_per_eu(3, 3))) void compress_persistent_argtable_kernel(
+    CompressParams p, ArgTable) {
+    compress_persistent<kQuant, kEarly>(p);
 }
 
 // ---- relative-bound pre-pass (jobs too long for the fused exchange) -------
@@ -2836,9 +2883,7 @@ __device__ __forceinline__ uint32_t run_start(const DecompressParams& p, uint32_
 }
 
 template <int kDst>
-__global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_persistent_kernel(
-    DecompressParams p) {
+__device__ __forceinline__ void decompress_persistent(const DecompressParams& p) {
     __shared__ uint32_t s_wave[kThreads / 64];
     __shared__ uint32_t s_red[kThreads / 64];
     __shared__ uint32_t s_hdr[kTileBlocks / 4];
@@ -2910,6 +2955,21 @@ __attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_
         ++t;
     }
     if (err) flag_error(p.error, p.error_marker, err);
+}
+
+template <int kDst>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void decompress_persistent_kernel(
+    DecompressParams p) {
+    decompress_persistent<kDst>(p);
+}
+
+// The same with the job records in the kernel arguments (jobs_inline == 2).
+template <int kDst>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_num_sgpr(74), amdgpu_waves_per_eu(8, 8))) void
+decompress_persistent_argtable_kernel(DecompressParams p, ArgTable) {
+    decompress_persistent<kDst>(p);
 }
 
 // ---- packed publication ------------------------------------------------------
@@ -3013,12 +3073,41 @@ static void launch_block(void (*kernel)(Args...), uint32_t grid, uint32_t block,
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream, args...);
 }
 
-// Job records a kernel of these parameters can read (0 when an inline table
-// is said to hold more than it can).
+// Job records a kernel of these parameters can read (0 when the table it is
+// told to read cannot hold them).  `table_bytes`: the bytes of job records
+// an ArgTable launch carries (0 for every other launch, whose kernels have
+// no ArgTable argument).
 template <class Params>
-static uint32_t readable_jobs(const Params& p) {
-    return p.jobs_inline ? (p.num_jobs <= (uint32_t)kInlineJobs ? p.num_jobs : 0u)
-                         : (p.jobs != nullptr ? p.num_jobs : 0u);
+static uint32_t readable_jobs(const Params& p, size_t table_bytes = 0) {
+    const uint64_t need = (uint64_t)p.num_jobs * sizeof(p.inline_jobs[0]);
+    switch (p.jobs_inline) {
+    case 0:
+        return p.jobs != nullptr ? p.num_jobs : 0u;
+    case 1:
+        return p.num_jobs <= (uint32_t)kInlineJobs ? p.num_jobs : 0u;
+    case 2:
+        return need <= table_bytes && table_bytes <= kArgTableBytes ? p.num_jobs : 0u;
+    default:
+        return 0u;
+    }
+}
+
+// Launches a kernel of parameters (Params, ArgTable) whose ArgTable starts
+// with the `table_bytes` bytes at `table` (the rest is never read).
+template <class Params>
+static hipError_t launch_argtable(void (*kernel)(Params, ArgTable), uint32_t grid,
+                                  uint32_t block, hipStream_t stream, hipEvent_t start,
+                                  hipEvent_t stop, const Params& p, const void* table,
+                                  size_t table_bytes) {
+    static thread_local ArgTable t;
+    if (table == nullptr || table_bytes > kArgTableBytes) return hipErrorInvalidValue;
+    std::memcpy(t.bytes, table, table_bytes);
+    void* args[] = {const_cast<Params*>(&p), &t};
+    if (start || stop)
+        return hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), dim3(grid),
+                                  dim3(block), args, 0, stream, start, stop, 0);
+    return hipLaunchKernel(reinterpret_cast<const void*>(kernel), dim3(grid), dim3(block),
+                           args, 0, stream);
 }
 
 template <class... Args>
@@ -3058,11 +3147,24 @@ hipError_t launch_compress(const CompressParams& p, hipStream_t stream,
 
 hipError_t launch_compress_pipelined(const CompressParams& p, uint32_t grid,
                                      hipStream_t stream, hipEvent_t start,
-                                     hipEvent_t stop) {
-    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true, readable_jobs(p)))
+                                     hipEvent_t stop, const void* table,
+                                     size_t table_bytes) {
+    const bool arg = p.jobs_inline == 2;
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true,
+                      readable_jobs(p, arg ? table_bytes : 0)))
         return hipErrorInvalidValue;
     uint32_t longest = 0;
     for (int i = 0; i < p.num_groups; ++i) longest = std::max(longest, p.groups[i].tiles_per_job);
+    if (arg) {
+        void (*k)(CompressParams, ArgTable) =
+            longest <= kEarlyLookbackTiles
+                ? (p.quantizer ? compress_persistent_argtable_kernel<1, true>
+                               : compress_persistent_argtable_kernel<0, true>)
+                : (p.quantizer ? compress_persistent_argtable_kernel<1, false>
+                               : compress_persistent_argtable_kernel<0, false>);
+        return launch_argtable(k, grid, kEncThreads, stream, start, stop, p, table,
+                               table_bytes);
+    }
     if (longest <= kEarlyLookbackTiles) {
         if (p.quantizer)
             launch_block(compress_persistent_kernel<1, true>, grid, kEncThreads, stream, start,
@@ -3094,9 +3196,19 @@ hipError_t launch_minmax(const MinMaxParams& p, uint32_t grid,
 
 hipError_t launch_decompress_persistent(const DecompressParams& p, uint32_t grid,
                                        hipStream_t stream, hipEvent_t start,
-                                       hipEvent_t stop) {
-    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true, readable_jobs(p)))
+                                       hipEvent_t stop, const void* table,
+                                       size_t table_bytes) {
+    const bool arg = p.jobs_inline == 2;
+    if (!tile_plan_ok(p.groups, p.num_groups, p.total_tiles, grid, true,
+                      readable_jobs(p, arg ? table_bytes : 0)))
         return hipErrorInvalidValue;
+    if (arg) {
+        void (*k)(DecompressParams, ArgTable) =
+            p.dst_kind == kDstMulti     ? decompress_persistent_argtable_kernel<kDstMulti>
+            : p.dst_kind == kDstIndexed ? decompress_persistent_argtable_kernel<kDstIndexed>
+                                        : decompress_persistent_argtable_kernel<kDstLinear>;
+        return launch_argtable(k, grid, kThreads, stream, start, stop, p, table, table_bytes);
+    }
     switch (p.dst_kind) {
     case kDstMulti:
         launch(decompress_persistent_kernel<kDstMulti>, grid, stream, start, stop, p);

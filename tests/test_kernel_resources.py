@@ -56,6 +56,15 @@ def kernels(tmp_path_factory):
             "lds": field("group_segment_fixed_size"),
             "scratch": field("private_segment_fixed_size"),
         }
+    # explicit (by_value) arguments of each kernel: (offset, size)
+    notes = text[text.index("amdhsa.kernels:"):]
+    for m in re.finditer(r"  - \.agpr_count:.*?\.args:\n(.*?)\n    \.[a-z_]+:.*?\.name:\s+(\S+)",
+                         notes, re.S):
+        if m.group(2) in meta:
+            meta[m.group(2)]["args"] = [
+                (int(o), int(z)) for o, z, kind in re.findall(
+                    r"\.offset:\s+(\d+)\n\s+\.size:\s+(\d+)\n\s+\.value_kind:\s+(\S+)",
+                    m.group(1)) if kind == "by_value"]
     return meta
 
 
@@ -66,7 +75,8 @@ def pick(meta, name):
 
 
 def test_persistent_decoder_fits_eight_waves(kernels):
-    for k, m in pick(kernels, "decompress_persistent_kernel").items():
+    for k, m in {**pick(kernels, "decompress_persistent_kernel"),
+                 **pick(kernels, "decompress_persistent_argtable_kernel")}.items():
         assert m["vgpr"] <= 64, (k, m)
         assert m["sgpr"] <= 74, (k, m)
         assert m["lds"] <= 20480, (k, m)
@@ -74,10 +84,27 @@ def test_persistent_decoder_fits_eight_waves(kernels):
 
 
 def test_persistent_encoder_fits_three_waves(kernels):
-    for k, m in pick(kernels, "compress_persistent_kernel").items():
+    for k, m in {**pick(kernels, "compress_persistent_kernel"),
+                 **pick(kernels, "compress_persistent_argtable_kernel")}.items():
         if "decompress" in k:
             continue
         assert m["vgpr"] <= 168, (k, m)
         assert m["sgpr"] <= 100, (k, m)
         assert 6 * m["lds"] <= 160 * 1024, (k, m)
         assert m["scratch"] == 0, (k, m)
+
+
+def test_arg_table_layout(kernels):
+    """The ArgTable launches read job records at arg_table_offset<Params>():
+    the parameter block rounded up to 16 bytes (kvszp_internal.h).  The
+    compiler must place the second argument exactly there, with the size
+    the host copies (kArgTableBytes), and the whole argument segment must
+    stay within what the runtime was measured to carry (16 648 bytes)."""
+    got = {**pick(kernels, "compress_persistent_argtable_kernel"),
+           **pick(kernels, "decompress_persistent_argtable_kernel")}
+    assert len(got) == 7  # 4 encoder and 3 decoder instantiations
+    for k, m in got.items():
+        (o0, z0), (o1, z1) = m["args"]
+        assert o0 == 0 and o1 == (z0 + 15) // 16 * 16, (k, m["args"])
+        assert z1 == 14336, (k, m["args"])
+        assert o1 + z1 <= 16648, (k, m["args"])
