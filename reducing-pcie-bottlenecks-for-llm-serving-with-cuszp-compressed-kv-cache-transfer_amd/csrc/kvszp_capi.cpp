@@ -112,6 +112,10 @@ struct kvszp_ctx {
     // Persistent encoder grid (co-resident workgroups); 0 = one workgroup
     // per tile (KVSZP_PERSISTENT=0, or ticket mode).
     uint32_t pipelined_grid = 0;
+    // Compute units of the device, and the persistent encoder's first-tile
+    // mapping (persistent_slot_cus mode; KVSZP_SLOT_MIX=0/1/2, default 1).
+    uint32_t cus = 0;
+    int slot_mix = 1;
     uint32_t decompress_grid = 0;   // persistent decoder grid (0 = off)
     // control words: [0] ticket counter, [1] low 32 bits = error word
     unsigned long long* control = nullptr;
@@ -596,6 +600,7 @@ int compress_groups(kvszp_ctx* c, const void* const* inputs,
         if (persistent) {
             p.ticket = nullptr;
             const uint32_t grid = (uint32_t)std::min<uint64_t>(ch.tiles, c->pipelined_grid);
+            p.slot_cus = persistent_slot_cus(ch.tiles, grid, c->cus, c->slot_mix);
             e = launch_compress_pipelined(p, grid, stream, timing_start(c, rec),
                                           timing_stop(c, rec), use_arg ? jobs.data() : nullptr,
                                           use_arg ? table_bytes : 0);
@@ -935,6 +940,12 @@ int kvszp_create(const kvszp_config* config, int device_id, kvszp_ctx** out) {
     const int resident = compress_resident_workgroups(device_id, false);
     c->fused_tile_limit = (uint32_t)std::min(kThreads, std::max(0, resident / 4));
     {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_id) ==
+                hipSuccess && cus > 0)
+            c->cus = (uint32_t)cus;
+        if (const char* mix = std::getenv("KVSZP_SLOT_MIX"))
+            c->slot_mix = mix[0] == '0' ? 0 : mix[0] == '2' ? 2 : 1;
         const char* env = std::getenv("KVSZP_PERSISTENT");
         const bool off = (env && env[0] == '0') || c->use_tickets;
         c->pipelined_grid =

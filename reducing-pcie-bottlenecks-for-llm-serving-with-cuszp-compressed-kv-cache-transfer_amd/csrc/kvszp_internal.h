@@ -120,6 +120,9 @@ struct CompressParams {
     int aligned16;                    // every input page is 16-byte aligned
     int input_f32;                    // pages hold fp32 values (not BF16)
     int mode;                         // fp32 pages: kModeFixed/Plain/Outlier
+    // Persistent encoder: the C of persistent_first_tile (0: workgroup b
+    // starts at tile b).
+    uint32_t slot_cus;
     // Time-bounded waits (persistent encoder, fused bound exchange): a wait
     // longer than wait_ticks of the steady clock stores the launch's epoch
     // in *abort_word and seq in host_ctl[kHostAbort], and every wait of the

@@ -1778,7 +1778,7 @@ __device__ __forceinline__ void compress_persistent(const CompressParams& p) {
     bool aborted = false;  // stop: the host encodes this launch again
 
     // Prologue: the first tile and its keys (published).
-    TileCtx cur = tile_ctx(p, blockIdx.x, s_gfirst);
+    TileCtx cur = tile_ctx(p, persistent_first_tile(blockIdx.x, G, p.slot_cus), s_gfirst);
     uint32_t D0[16], D1[16], N0[16], N1[16];
     // Keys of the current tile's blocks: the published keys, except that a
     // block holding a NaN keeps the keys of -inf and +inf (kNanRateKeys),

@@ -282,6 +282,45 @@ int main() {
         reset(); g[0].tiles_per_job_div = Divisor{0, 0}; CHECK(!tile_plan_ok(g, ng, 17, 17, false, 9), "missing divisor accepted");
     }
 
+    // The persistent encoder's first tiles: a permutation of 0 .. G - 1 for
+    // every grid of S workgroups on C units, so that the workgroups' walks
+    // f, f + G, ... cover every tile of a launch exactly once; and the
+    // launches that take the unit-major order.
+    {
+        long walked = 0;
+        for (uint32_t C : {1u, 2u, 8u, 80u, 256u, 304u}) {
+            for (uint32_t S = 1; S <= 8; ++S) {
+                const uint32_t G = C * S;
+                std::vector<int> seen(G, 0);
+                for (uint32_t b = 0; b < G; ++b) {
+                    const uint32_t f = persistent_first_tile(b, G, C);
+                    CHECK(f < G, "C %u S %u: workgroup %u starts at %u", C, S, b, f);
+                    if (f < G) seen[f] += 1;
+                    if (S > 1 && b % C + 1 < C)  // unit r holds tiles r*S .. r*S + S - 1
+                        CHECK(persistent_first_tile(b + 1, G, C) == f + S, "C %u S %u b %u", C, S, b);
+                }
+                for (uint32_t f = 0; f < G; ++f) CHECK(seen[f] == 1, "C %u S %u: tile %u", C, S, f);
+                for (uint64_t T : {(uint64_t)G, (uint64_t)G + 1, (uint64_t)4 * G + G / 3 + 1, (uint64_t)17 * G - 1}) {
+                    std::vector<int> cover(T, 0);
+                    for (uint32_t b = 0; b < G; ++b)
+                        for (uint64_t t = persistent_first_tile(b, G, C); t < T; t += G) cover[t] += 1;
+                    for (uint64_t t = 0; t < T; ++t) CHECK(cover[t] == 1, "C %u S %u T %llu: tile %llu", C, S,
+                                                           (unsigned long long)T, (unsigned long long)t);
+                    walked += (long)T;
+                }
+            }
+        }
+        // Qwen2.5-1.5B 4K (7168 tiles) keeps workgroup order on 1536 = 6 x 256;
+        // the 8192-page pool (229376 tiles) and longer take the unit-major order.
+        CHECK(persistent_slot_cus(7168, 1536, 256, 1) == 0, "short launch mixed");
+        CHECK(persistent_slot_cus(229376, 1536, 256, 1) == 256, "long launch not mixed");
+        CHECK(persistent_slot_cus(7168, 1536, 256, 2) == 256, "mode 2");
+        CHECK(persistent_slot_cus(229376, 1536, 256, 0) == 0, "mode 0");
+        CHECK(persistent_slot_cus(229376, 1500, 256, 1) == 0, "grid not a multiple of the units");
+        CHECK(persistent_slot_cus(229376, 256, 256, 1) == 0, "one workgroup per unit");
+        std::printf("first-tile walks=%ld\n", walked);
+    }
+
     std::printf("launches=%ld tiles=%ld mismatches=%ld\n", launches, tiles_checked, g_bad);
     return g_bad == 0 ? 0 : 1;
 }
