@@ -770,27 +770,27 @@ int decompress_groups(kvszp_ctx* c, const void* const* compressed,
     const size_t jobs_bytes = (batch * sizeof(DecompressJob) + 255) & ~(size_t)255;
     const size_t dests_bytes = dest_table.size() * sizeof(uint16_t*);
     const size_t runs_off = (jobs_bytes + dests_bytes + 15) & ~(size_t)15;
-    std::vector<char> table(runs.empty() ? jobs_bytes + dests_bytes
-                                         : runs_off + runs.size() * sizeof(uint32_t));
-    std::memcpy(table.data(), jobs.data(), batch * sizeof(DecompressJob));
-    if (!dest_table.empty())
-        std::memcpy(table.data() + jobs_bytes, dest_table.data(), dests_bytes);
-    if (!runs.empty())
-        std::memcpy(table.data() + runs_off, runs.data(), runs.size() * sizeof(uint32_t));
     if ((rc = ensure(c->tile_state, max_tiles * 8, true, stream))) return rc;
     const uint32_t seq = ++c->seq;
     // Small calls without a destination table or run starts pass their job
     // table in the kernel arguments (no upload), and so does a persistent
     // launch whose job table (no destination table, no run starts) fits an
-    // ArgTable.
+    // ArgTable.  Only the other calls build and upload the packed table.
     const bool inline_jobs =
         batch <= (size_t)kInlineJobs && dest_table.empty() && runs.empty();
     const size_t job_bytes = batch * sizeof(DecompressJob);
     const bool arg_table = !inline_jobs && (c->arg_tables & 2) && persistent &&
                            dest_table.empty() && runs.empty() && job_bytes <= kArgTableBytes;
-    if (!inline_jobs && !arg_table &&
-        (rc = upload_tables(c, table.data(), table.size(), seq, stream)))
-        return rc;
+    if (!inline_jobs && !arg_table) {
+        std::vector<char> table(runs.empty() ? jobs_bytes + dests_bytes
+                                             : runs_off + runs.size() * sizeof(uint32_t));
+        std::memcpy(table.data(), jobs.data(), batch * sizeof(DecompressJob));
+        if (!dest_table.empty())
+            std::memcpy(table.data() + jobs_bytes, dest_table.data(), dests_bytes);
+        if (!runs.empty())
+            std::memcpy(table.data() + runs_off, runs.data(), runs.size() * sizeof(uint32_t));
+        if ((rc = upload_tables(c, table.data(), table.size(), seq, stream))) return rc;
+    }
 
     size_t first_job = 0;
     for (const Chunk& ch : chunks) {
