@@ -775,8 +775,8 @@ def main() -> int:
         return traffic_from(args.traffic_from, args.config)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (KV pages "
-              "are private to the GPU that owns them; see DESIGN.md for how the "
-              "path shards).", file=sys.stderr)
+              "are private to the GPU that owns them, and each GPU's connector stores "
+              "and restores its own pages).", file=sys.stderr)
         return 2
 
     import torch
