@@ -1197,11 +1197,11 @@ int kvszp_compress_batch_fixed_bf16_noalloc(
         p.abort_word = words + kScratchAbort / 8;
         p.wait_ticks = c->wait_ticks;
     }
-    if (persistent)
-        e = launch_compress_pipelined(
-            p, (uint32_t)std::min<uint64_t>(p.total_tiles, c->pipelined_grid), stream,
-            nullptr, nullptr);
-    else
+    if (persistent) {
+        const uint32_t grid = (uint32_t)std::min<uint64_t>(p.total_tiles, c->pipelined_grid);
+        p.slot_cus = persistent_slot_cus(p.total_tiles, grid, c->cus, c->slot_mix);
+        e = launch_compress_pipelined(p, grid, stream, nullptr, nullptr);
+    } else
         e = launch_compress(p, stream, nullptr, nullptr);
     if (e != hipSuccess) return hip_fail(e, "compress launch");
     e = wait_stream(stream);

@@ -21,12 +21,24 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _ctx(relative=True):
+def _ctx(relative=True, slot_mix=None):
+    import os
+
     import kvszp
 
     cfg = kvszp.Config(1e-4, 1 if relative else 0, kvszp.DIM_1D,
                        kvszp.MODE_FIXED, kvszp.TYPE_FLOAT)
-    return kvszp.Context(cfg, 0)
+    old = os.environ.get("KVSZP_SLOT_MIX")
+    if slot_mix is not None:
+        os.environ["KVSZP_SLOT_MIX"] = slot_mix
+    try:
+        return kvszp.Context(cfg, 0)
+    finally:
+        if slot_mix is not None:
+            if old is None:
+                del os.environ["KVSZP_SLOT_MIX"]
+            else:
+                os.environ["KVSZP_SLOT_MIX"] = old
 
 
 def _pages(batch, n, seed):
@@ -59,13 +71,17 @@ def test_noalloc_matches_allocating_entry_point(relative):
 
     ctx = _ctx(relative)
     other = _ctx(relative)   # a second context shares the GPU's scratch array
+    # the persistent encoder in unit-major tile order (1024 tiles on a grid
+    # of 4 workgroups per compute unit)
+    mixed = _ctx(relative, slot_mix="2")
     # two calls in a row, the second smaller; then a long page (min/max
-    # pre-pass mode) and a call from the other context
+    # pre-pass mode), a call from the other context and one in unit-major order
     for c, (batch, n, seed) in ((ctx, (6, 229376, 1)), (ctx, (3, 36864, 2)),
-                                (ctx, (2, 2_500_032, 3)), (other, (5, 8192 * 3 + 64, 4))):
+                                (ctx, (2, 2_500_032, 3)), (other, (5, 8192 * 3 + 64, 4)),
+                                (mixed, (128, 65536, 5))):
         pages = _pages(batch, n, seed)
-        eps = [1e-4, 1e-5, 3e-4, 1e-4, 2e-4, 1e-4][:batch] if relative else \
-              [1e-3, 2e-2, 5e-4, 1e-3, 1e-3, 1e-3][:batch]
+        eps = ([1e-4, 1e-5, 3e-4, 1e-4, 2e-4, 1e-4] * 22)[:batch] if relative else \
+              ([1e-3, 2e-2, 5e-4, 1e-3, 1e-3, 1e-3] * 22)[:batch]
         s1, b1, d1 = _run(kvszp, c, True, pages, eps)
         s2, b2, d2 = _run(kvszp, c, False, pages, eps)
         assert s1 == s2, (batch, n)
