@@ -15,6 +15,8 @@ filled with 0xAB first).
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -23,7 +25,8 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 CONFIG_EB = 1e-4          # the wrappers' configured bound (eps <= 0 or NaN)
-SEEDS = range(64)
+# KVSZP_SWEEP_SEEDS=n widens the sweep to seeds 0 .. n-1 (64 by default)
+SEEDS = range(int(os.environ.get("KVSZP_SWEEP_SEEDS", "64")))
 
 EXTREME_ABS = [1e-40, 1e-45, 2e-39, float("inf"), float("nan"), 0.0, -1.0, 3e38]
 EXTREME_REL = [1e-40, 1e-45, 3e-39, float("inf"), float("nan"), 0.0, -1.0, 1e30]
