@@ -109,3 +109,56 @@ def test_noalloc_rejects_calls_beyond_its_limits():
     # the context still works afterwards
     s, _, d = _run(kvszp, ctx, True, _pages(2, 8192, 7), [1e-4, 1e-4])
     assert all(v > 0 for v in s)
+
+
+_CTXS = {}
+
+
+def _cached_ctx(relative):
+    if relative not in _CTXS:
+        _CTXS[relative] = _ctx(relative)
+    return _CTXS[relative]
+
+
+def _random_pages(rng, batch, n):
+    rows = []
+    for _ in range(batch):
+        kind = rng.choice(["gauss", "gauss", "gauss", "zero", "constant", "wide"])
+        if kind == "zero":
+            rows.append(np.zeros(n, np.float32))
+        elif kind == "constant":
+            rows.append(np.full(n, rng.choice([0.8125, -3.5, 1e-3]), np.float32))
+        elif kind == "wide":
+            rows.append((rng.standard_normal(n) * 10.0 ** rng.integers(-3, 4)).astype(np.float32))
+        else:
+            rows.append((rng.standard_normal(n) * np.exp(rng.standard_normal())).astype(np.float32))
+    return torch.from_numpy(np.stack(rows)).to(torch.bfloat16).to(DEV)
+
+
+# KVSZP_NOALLOC_SEEDS=n widens the sweep below to seeds 0 .. n-1 (16 by default)
+_NOALLOC_SEEDS = range(int(__import__("os").environ.get("KVSZP_NOALLOC_SEEDS", "16")))
+
+
+@pytest.mark.parametrize("seed", _NOALLOC_SEEDS)
+def test_noalloc_random_shapes_match_allocating_entry_point(seed):
+    """Seeded shapes, two calls in a row on the same scratch array: segment
+    lengths off the block and tile sizes, 1-24 pages, relative and absolute
+    bounds (eps 0 and negative fall back to the configured bound), zero and
+    constant pages."""
+    import kvszp
+
+    rng = np.random.default_rng(1000 + seed)
+    relative = bool(rng.integers(2))
+    ctx = _cached_ctx(relative)
+    for _ in range(2):
+        n = int(rng.choice([1, 31, 32, 33, 8191, 8192, 8193, 36864, 65553, 229376]))
+        batch = int(rng.integers(1, 25 if n <= 65553 else 9))
+        pages = _random_pages(rng, batch, n)
+        pool = [1e-4, 1e-5, 3e-3, 0.0, -1.0] if relative else [1e-3, 1e-2, 5e-5, 0.5, 0.0]
+        eps = [float(rng.choice(pool)) for _ in range(batch)]
+        s1, b1, d1 = _run(kvszp, ctx, True, pages, eps)
+        s2, b2, d2 = _run(kvszp, ctx, False, pages, eps)
+        assert s1 == s2, (seed, batch, n)
+        assert [np.float32(v) for v in b1] == [np.float32(v) for v in b2], (seed, batch, n)
+        for i in range(batch):
+            assert np.array_equal(d1[i], d2[i]), (seed, batch, n, i)
