@@ -378,3 +378,55 @@ def test_random_packed_store_and_restore(cpp, oracle, seed):
             prefix, src, epl, bounds)
         assert w.synchronize()
         assert np.array_equal(u16(dest), want)
+
+
+# KVSZP_SWEEP_LARGE_SEEDS=n widens the large grouped restore below (4 seeds by default)
+LARGE_SEEDS = range(int(os.environ.get("KVSZP_SWEEP_LARGE_SEEDS", "4")))
+
+
+@pytest.mark.parametrize("seed", LARGE_SEEDS)
+def test_random_large_grouped_restore(cpp, oracle, seed):
+    """Grouped indexed store, then one grouped indexed-scatter restore of
+    2400-6000 tiles: more tiles than the persistent decoder's grid, so its
+    workgroup runs start inside jobs of the groups' different tile counts
+    (layer sizes off the block size); 60-600 requests, so job tables travel
+    in the kernel arguments or, above 597 requests, are copied.  Every
+    restored value equals the oracle's decode of its stream."""
+    rng = np.random.default_rng(9000 + seed)
+    prefix, src = 2, int(rng.integers(8, 29))
+    epl = int(rng.integers(6000, 20001))
+    order = [int(v) for v in rng.permutation(src)]
+    ngroups = int(rng.integers(1, 4))
+    cuts = sorted(int(v) for v in rng.choice(np.arange(1, src), size=ngroups - 1,
+                                             replace=False))
+    groups = [sorted(order[a:b]) for a, b in zip([0] + cuts, cuts + [src])]
+    tile = 8192
+    tiles_per_page = sum(-(-prefix * len(g) * epl // tile) for g in groups)
+    target = int(rng.integers(2500, 6001))
+    pages_n = max(1, min(600 // ngroups, -(-target // tiles_per_page)))
+    pages = bf16_pages(rng, pages_n, prefix * src * epl,
+                       str(rng.choice(["normal", "offset", "special"])))
+    inputs, eps, idx, counts, ns = [], [], [], [], []
+    for layers in groups:
+        inputs += list(pages)
+        eps += [float(rng.choice([1e-3, 1e-4, 1e-5]))] * pages_n
+        idx.append(torch.tensor(layers, dtype=torch.long, device=DEV))
+        counts.append(pages_n)
+        ns.append(prefix * len(layers) * epl)
+    assert sum(pages_n * -(-m // tile) for m in ns) > 2048
+    bufs = [b for m in ns for b in canary_buffers(oracle, pages_n, m)]
+    w = wrapper(cpp, True)
+    ok, sizes, bounds = w.compress_batch_fixed_bf16_indexed_groups(inputs, bufs, idx, counts,
+                                                                   prefix, src, epl, eps)
+    assert ok
+    dest = torch.zeros_like(pages)
+    assert w.decompress_batch_fixed_bf16_indexed_scatter_groups(
+        bufs, sizes, list(dest) * len(groups), idx, counts, prefix, src, epl, bounds)
+    assert w.synchronize()
+    want = np.zeros((pages_n, prefix * src * epl), dtype=np.uint16)
+    for gi, layers in enumerate(groups):
+        for p in range(pages_n):
+            k = gi * pages_n + p
+            oracle.decompress_indexed(bufs[k][:sizes[k]].cpu().numpy(), ns[gi],
+                                      float(bounds[k]), want[p], layers, src, epl)
+    assert np.array_equal(u16(dest), want)
