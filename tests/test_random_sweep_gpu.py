@@ -391,7 +391,8 @@ def test_random_large_grouped_restore(cpp, oracle, seed):
     workgroup runs start inside jobs of the groups' different tile counts
     (layer sizes off the block size); 60-600 requests, so job tables travel
     in the kernel arguments or, above 597 requests, are copied.  Every
-    restored value equals the oracle's decode of its stream."""
+    stream and bound equals the oracle's, and every restored value the
+    oracle's decode of its stream."""
     rng = np.random.default_rng(9000 + seed)
     prefix, src = 2, int(rng.integers(8, 29))
     epl = int(rng.integers(6000, 20001))
@@ -419,6 +420,12 @@ def test_random_large_grouped_restore(cpp, oracle, seed):
     ok, sizes, bounds = w.compress_batch_fixed_bf16_indexed_groups(inputs, bufs, idx, counts,
                                                                    prefix, src, epl, eps)
     assert ok
+    # the store: a persistent encoder launch of several rounds over the same jobs
+    bits = u16(pages)
+    for gi, layers in enumerate(groups):
+        k = slice(gi * pages_n, (gi + 1) * pages_n)
+        check_streams(oracle, bits, ns[gi], bufs[k], sizes[k], bounds[k], eps[k], True, 0,
+                      layers, src, epl)
     dest = torch.zeros_like(pages)
     assert w.decompress_batch_fixed_bf16_indexed_scatter_groups(
         bufs, sizes, list(dest) * len(groups), idx, counts, prefix, src, epl, bounds)
